@@ -1,0 +1,195 @@
+/*
+ * pai_hip — MI355X (gfx950) quantized-weights matmul behind ProsperoAI's
+ * C operator interface.
+ *
+ * Computes y[M][N] = x[M][K] · Wᵀ where W[N][K] is stored as GGUF blocks
+ * (Q8_0, Q4_0, Q4_K, Q6_K) in the native GGUF row layout, x and y are f32
+ * row-major. This is the GPU twin of the reference's per-projection CPU
+ * operator, which is the composition
+ *     pai_gguf_dequant     (adapters/llama/gguf.c:969-1012, blocks → f32)
+ *   → transpose2d          (adapters/llama/llama.c:196-209, [N][K] → [K][N])
+ *   → pai_ref_gemm_f32     (cpu/reference/ref_ops.c:427-444)
+ * called from the executor's run_gemm (scheduler/scheduler.c:285-343).
+ *
+ * ABI conventions follow cpu/optimized/opt_ops.h:36-81 and
+ * cpu/reference/ref_ops.h: free C functions, uint64_t dimensions, raw
+ * pointers, pai_status_t returns; PAI_ERR_INVALID_ARG for NULL pointers or
+ * zero dimensions; the caller owns x and y. No call aborts the process:
+ * HIP failures map to PAI_ERR_INIT / NOMEM / INTERNAL / TIMEOUT.
+ *
+ * Thread-safety: init/shutdown are idempotent and serialised internally.
+ * Calls on different pai_qmat_t handles may run concurrently; the
+ * synchronous entry points use one internal stream per calling thread.
+ */
+#ifndef PAI_HIP_H
+#define PAI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: same type and values as sdk/include/pai/error.h:11-23, so a
+ * caller that already includes <pai/error.h> sees identical definitions. */
+typedef int32_t pai_status_t;
+#ifndef PAI_OK
+#define PAI_OK 0
+#define PAI_ERR_INVALID_ARG -1
+#define PAI_ERR_NOMEM -2
+#define PAI_ERR_UNSUPPORTED -3
+#define PAI_ERR_CAPABILITY -4
+#define PAI_ERR_TIMEOUT -5
+#define PAI_ERR_MISMATCH -6
+#define PAI_ERR_IO -7
+#define PAI_ERR_INIT -8
+#define PAI_ERR_INTERNAL -9
+#define PAI_ERR_PROTOCOL -10
+#endif
+
+/* Block formats accepted by pai_qmat_upload. The values are the ggml type
+ * ids used in GGUF files (adapters/llama/gguf.h:34-51: Q4_0 = 2, Q8_0 = 8,
+ * Q4_K = 12, Q6_K = 14); other ids return PAI_ERR_UNSUPPORTED. */
+#define PAI_QTYPE_Q4_0 2u
+#define PAI_QTYPE_Q8_0 8u
+#define PAI_QTYPE_Q4_K 12u
+#define PAI_QTYPE_Q6_K 14u
+
+/* ---------------------------------------------------------------------- */
+/* Lifecycle                                                               */
+/* ---------------------------------------------------------------------- */
+
+/* Select the current HIP device, check it is gfx950 and load the kernels.
+ * Idempotent; PAI_ERR_INIT when no usable device is present.
+ * Replaces nothing in the reference (its runtime has no GPU bring-up on
+ * this path; runtime/runtime.c:17-81 is the CPU analogue). */
+pai_status_t pai_hip_init(void);
+
+/* Release the per-thread streams. Idempotent. Handles stay valid only
+ * until their pai_qmat_free. */
+pai_status_t pai_hip_shutdown(void);
+
+/* Human-readable text of the last failure on this thread ("" if none). */
+const char *pai_hip_last_error(void);
+
+/* Bytes occupied by `numel` elements of `type`; 0 when numel is not a
+ * whole number of blocks or the type is not one of the four above.
+ * Same semantics as pai_gguf_type_bytes (adapters/llama/gguf.c:562-597)
+ * restricted to those types. */
+uint64_t pai_qtype_bytes(uint32_t type, uint64_t numel);
+
+/* ---------------------------------------------------------------------- */
+/* Packed weights resident in HBM                                          */
+/* ---------------------------------------------------------------------- */
+
+typedef struct pai_qmat pai_qmat_t;
+
+/* Copy W[N][K] in native GGUF block layout (N rows of K/blk blocks, the
+ * bytes pai_gguf_dequant reads at adapters/llama/gguf.c:1003) from host
+ * memory into device memory, re-laid out for the kernels. Dequantized
+ * values are unchanged, bit for bit.
+ * Replaces the session-init load (models/model.c:242-298) for GGUF-tagged
+ * weights: the blocks are uploaded instead of being dequantized into the
+ * host region.
+ * Errors: INVALID_ARG (NULL, zero dims), UNSUPPORTED (type, or K not a
+ * whole number of blocks), MISMATCH (nbytes != N * pai_qtype_bytes(K)),
+ * NOMEM (device allocation), INIT (no device). */
+pai_status_t pai_qmat_upload(pai_qmat_t **out, uint32_t type, uint64_t n,
+                             uint64_t k, const void *blocks, uint64_t nbytes);
+
+/* Same, from native blocks already in device memory (`stream` is a
+ * hipStream_t or NULL for the calling thread's stream; the call returns
+ * after the re-layout completes). */
+pai_status_t pai_qmat_upload_device(pai_qmat_t **out, uint32_t type,
+                                    uint64_t n, uint64_t k,
+                                    const void *dev_blocks, uint64_t nbytes,
+                                    void *stream);
+
+/* Free the device copy. NULL is a no-op returning PAI_OK. */
+pai_status_t pai_qmat_free(pai_qmat_t *w);
+
+/* Type and shape of a handle. */
+pai_status_t pai_qmat_shape(const pai_qmat_t *w, uint32_t *type, uint64_t *n,
+                            uint64_t *k);
+
+/* Packed bytes of the matrix (N * pai_qtype_bytes(K)); 0 for NULL. */
+uint64_t pai_qmat_bytes(const pai_qmat_t *w);
+
+/* ---------------------------------------------------------------------- */
+/* Compute                                                                  */
+/* ---------------------------------------------------------------------- */
+
+/* flags for pai_qgemm_f32 / pai_qdequant_f32 */
+#define PAI_QGEMM_DEVICE_PTRS (1u << 0) /* x, y (out) are device pointers  */
+#define PAI_QGEMM_MFMA_BF16 (1u << 1)   /* M >= 32: bf16 MFMA operands      */
+#define PAI_QGEMM_FP32 (1u << 2)        /* any M: f32 dequant + f32 FMA path */
+
+/* y[m][n] = sum_k x[m][k] * W[n][k], x: [M][K] f32, y: [M][N] f32.
+ *  - M < 32 (or PAI_QGEMM_FP32): blocks are dequantized in registers and
+ *    multiplied in f32 with f32 accumulation. Matches the reference's
+ *    sequential f32 sum within rel-L2 1e-5.
+ *  - M >= 32: dequantized tiles are staged in LDS as fp16 (default) or
+ *    bf16 and multiplied on MFMA with f32 accumulation. Tolerance:
+ *    rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16).
+ * Without PAI_QGEMM_DEVICE_PTRS, x and y are host pointers and the call
+ * copies them; with it, they are device pointers. Synchronous.
+ * Replaces pai_ref_gemm_f32 at scheduler/scheduler.c:340 for a weight
+ * value carrying the GGUF tag, i.e. the composition described above. */
+pai_status_t pai_qgemm_f32(const pai_qmat_t *w, uint64_t m, const float *x,
+                           float *y, uint32_t flags);
+
+/* Asynchronous form: x and y must be device pointers; `stream` is a
+ * hipStream_t (NULL = the default stream). Returns once the kernels are
+ * enqueued; argument and shape errors are reported before any launch. */
+pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
+                                 const float *x, float *y, uint32_t flags,
+                                 void *stream);
+
+/* out[N][K] = dequantized W in the native element order, computed on the
+ * GPU from the device copy; bit-identical to pai_gguf_dequant
+ * (adapters/llama/gguf.c:650-967) for every row. Host pointer unless
+ * PAI_QGEMM_DEVICE_PTRS. Synchronous. */
+pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags);
+
+/* ---------------------------------------------------------------------- */
+/* Op-registry descriptors                                                  */
+/* ---------------------------------------------------------------------- */
+
+/* Capability bit for ops with a HIP implementation on gfx950. The
+ * reference defines bits 0-2 (sdk/include/pai/op.h:59-61). */
+#define PAI_OP_CAP_GPU_HIP (1u << 3)
+
+/* Same field order, types and size as pai_op_descriptor_t
+ * (sdk/include/pai/op.h:71-82), so a pointer to one of these can be
+ * passed to pai_op_registry_register (runtime/op_registry.c) unchanged.
+ * The dtype fields hold pai_dtype_t values (sdk/include/pai/dtype.h:12-23;
+ * 0 = PAI_DTYPE_F32, 8 = PAI_DTYPE_U8). */
+typedef struct pai_hip_op_descriptor {
+  const char *name;
+  uint32_t version;
+  uint32_t num_inputs;
+  uint32_t num_outputs;
+  int32_t in_dtype;
+  int32_t out_dtype;
+  uint32_t caps;
+  pai_status_t (*ref_fn)(void);
+  int32_t kernel_id;
+  uint32_t reserved[2];
+} pai_hip_op_descriptor_t;
+
+/* The four GPU descriptors "qgemm_q4_0_f32", "qgemm_q8_0_f32",
+ * "qgemm_q4_k_f32", "qgemm_q6_k_f32" (inputs: x f32, packed weight u8;
+ * output y f32; caps PAI_OP_CAP_GPU_HIP; ref_fn NULL, because the CPU
+ * path for these weights stays the reference's own dequant-at-import
+ * followed by pai_ref_gemm_f32; kernel_id PAI_KERNEL_NONE). The array is
+ * static and outlives any registry it is registered into. */
+const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count);
+
+/* Registry name for a ggml type ("qgemm_q4_k_f32"), NULL if unsupported. */
+const char *pai_hip_op_name(uint32_t type);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAI_HIP_H */

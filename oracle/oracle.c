@@ -1,0 +1,567 @@
+/*
+ * CPU oracle for the quantized-weights matmul. TEST INFRASTRUCTURE ONLY:
+ * loaded by tests/, the smoke check and the benchmark's CPU-baseline leg,
+ * never by the product library. See oracle.h for what pins each function.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; the AVX2 restatements
+ * carry their own target attribute, as the reference's do).
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------- */
+/* Scalars                                                                  */
+/* ---------------------------------------------------------------------- */
+
+/* IEEE binary16 -> binary32 by bit manipulation.
+ * Follows adapters/llama/gguf.c:601-630: signed zero, subnormals
+ * renormalised by shifting the mantissa until the implicit bit appears,
+ * inf/NaN keep the payload shifted left by 13. */
+float orc_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t e = ((uint32_t)h >> 10) & 0x1Fu;
+  uint32_t f = (uint32_t)h & 0x3FFu;
+  uint32_t bits;
+  float out;
+  if (e == 0u && f == 0u) {
+    bits = sign;
+  } else if (e == 0u) {
+    /* subnormal: value = f * 2^-24; normalise */
+    uint32_t ex = 113u; /* 127 - 15 + 1 */
+    while ((f & 0x400u) == 0u) {
+      f <<= 1;
+      ex -= 1u;
+    }
+    bits = sign | (ex << 23) | ((f & 0x3FFu) << 13);
+  } else if (e == 0x1Fu) {
+    bits = sign | 0x7F800000u | (f << 13);
+  } else {
+    bits = sign | ((e + 112u) << 23) | (f << 13);
+  }
+  memcpy(&out, &bits, sizeof out);
+  return out;
+}
+
+/* Bulk form writing raw bit patterns (a float return value would be
+ * widened to double by some callers, which quiets signalling NaNs). */
+void orc_f16_to_f32_bits(const uint16_t *h, uint32_t *out, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) {
+    const float f = orc_f16_to_f32(h[i]);
+    memcpy(&out[i], &f, sizeof f);
+  }
+}
+
+static float le_half(const uint8_t *p) {
+  return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+}
+
+/* Round-to-nearest-even binary32 -> binary16 (for the textbook encoders
+ * below; the reference has no f32->f16 encoder). */
+static uint16_t f32_to_f16_rne(float v) {
+  uint32_t x;
+  memcpy(&x, &v, sizeof x);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) { /* inf / nan */
+    return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+  }
+  if (ax >= 0x477FF000u) { /* rounds to >= 65520 -> inf */
+    return (uint16_t)(sign | 0x7C00u);
+  }
+  if (ax < 0x38800000u) { /* below the smallest normal half: subnormal */
+    /* value in units of 2^-24, rounded to nearest even */
+    float a;
+    memcpy(&a, &ax, sizeof a);
+    float scaled = a * 16777216.0f; /* exact: power of two */
+    float r = nearbyintf(scaled);   /* default rounding mode: RNE */
+    return (uint16_t)(sign | (uint16_t)r);
+  }
+  uint32_t e = (ax >> 23) - 112u;
+  uint32_t mant = ax & 0x7FFFFFu;
+  uint32_t h = (e << 10) | (mant >> 13);
+  uint32_t rest = mant & 0x1FFFu;
+  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) {
+    h += 1u; /* carries into the exponent correctly */
+  }
+  return (uint16_t)(sign | h);
+}
+
+/* 6-bit (scale, min) pair j of a Q4_K super-block's 12 packed bytes.
+ * Follows adapters/llama/gguf.c:639-648. */
+void orc_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn) {
+  if (j >= 4) {
+    *sc = (uint8_t)((q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4));
+    *mn = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+  } else {
+    *sc = (uint8_t)(q[j] & 0x3F);
+    *mn = (uint8_t)(q[j + 4] & 0x3F);
+  }
+}
+
+/* Bytes of `numel` elements; 0 when numel is not a whole number of
+ * blocks or the type is not one of the four on this path.
+ * Follows adapters/llama/gguf.c:562-597 (Q4_0 :571, Q8_0 :578,
+ * Q4_K :586, Q6_K :590). */
+uint64_t orc_type_bytes(uint32_t type, uint64_t numel) {
+  switch (type) {
+  case ORC_Q4_0:
+    return (numel % 32u) ? 0u : numel / 32u * 18u;
+  case ORC_Q8_0:
+    return (numel % 32u) ? 0u : numel / 32u * 34u;
+  case ORC_Q4_K:
+    return (numel % 256u) ? 0u : numel / 256u * 144u;
+  case ORC_Q6_K:
+    return (numel % 256u) ? 0u : numel / 256u * 210u;
+  default:
+    return 0u;
+  }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Block dequantization                                                     */
+/* ---------------------------------------------------------------------- */
+
+/* Q4_0, adapters/llama/gguf.c:680-694: 18-byte block = f16 d + 16 bytes;
+ * byte j holds element j (low nibble) and element j+16 (high nibble),
+ * both offset by 8; value = (float)(nibble-8) * d. */
+static void dq_q4_0(const uint8_t *blk, float *out) {
+  const float d = le_half(blk);
+  for (int j = 0; j < 16; ++j) {
+    const uint8_t b = blk[2 + j];
+    out[j] = (float)((int)(b & 0x0F) - 8) * d;
+    out[j + 16] = (float)((int)(b >> 4) - 8) * d;
+  }
+}
+
+/* Q8_0, adapters/llama/gguf.c:750-761: f16 d + 32 int8; value = q * d. */
+static void dq_q8_0(const uint8_t *blk, float *out) {
+  const float d = le_half(blk);
+  for (int j = 0; j < 32; ++j) {
+    out[j] = (float)(int8_t)blk[2 + j] * d;
+  }
+}
+
+/* Q4_K, adapters/llama/gguf.c:852-882: 144-byte super-block = f16 d,
+ * f16 dmin, 12 bytes of packed 6-bit (scale, min), 128 bytes of codes.
+ * Chunk c (64 elements) uses bytes q[32c .. 32c+32): low nibbles are
+ * elements 64c+l with pair 2c, high nibbles are 64c+32+l with pair 2c+1.
+ * The reference forms d1 = d*sc and m1 = dmin*m first, then d1*q - m1. */
+static void dq_q4_k(const uint8_t *blk, float *out) {
+  const float d = le_half(blk);
+  const float dmin = le_half(blk + 2);
+  const uint8_t *scales = blk + 4;
+  const uint8_t *q = blk + 16;
+  for (int c = 0; c < 4; ++c) {
+    uint8_t s0, m0, s1, m1;
+    orc_scale_min_k4(2 * c, scales, &s0, &m0);
+    orc_scale_min_k4(2 * c + 1, scales, &s1, &m1);
+    const float dlo = d * (float)s0, mlo = dmin * (float)m0;
+    const float dhi = d * (float)s1, mhi = dmin * (float)m1;
+    for (int l = 0; l < 32; ++l) {
+      out[64 * c + l] = dlo * (float)(q[32 * c + l] & 0x0F) - mlo;
+    }
+    for (int l = 0; l < 32; ++l) {
+      out[64 * c + 32 + l] = dhi * (float)(q[32 * c + l] >> 4) - mhi;
+    }
+  }
+}
+
+/* Q6_K, adapters/llama/gguf.c:920-947: 210-byte super-block = ql[128],
+ * qh[64], int8 scales[16], f16 d. Two halves of 128 elements; in half h,
+ * for l < 32 the four 6-bit codes are
+ *   e = l      : ql[l] low nibble,    qh[l] bits 0-1, scale sc[l/16 + 0]
+ *   e = l + 32 : ql[l+32] low nibble, qh[l] bits 2-3, scale sc[l/16 + 2]
+ *   e = l + 64 : ql[l] high nibble,   qh[l] bits 4-5, scale sc[l/16 + 4]
+ *   e = l + 96 : ql[l+32] high nibble,qh[l] bits 6-7, scale sc[l/16 + 6]
+ * with ql/qh/sc advanced by 64/32/8 per half; value = d * sc * (code-32),
+ * evaluated left to right. */
+static void dq_q6_k(const uint8_t *blk, float *out) {
+  const float d = le_half(blk + 208);
+  for (int h = 0; h < 2; ++h) {
+    const uint8_t *ql = blk + 64 * h;
+    const uint8_t *qh = blk + 128 + 32 * h;
+    const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+    float *o = out + 128 * h;
+    for (int l = 0; l < 32; ++l) {
+      const int s = l / 16;
+      const int c0 = (int)((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+      const int c1 = (int)((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+      const int c2 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+      const int c3 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+      o[l] = d * (float)sc[s + 0] * (float)c0;
+      o[l + 32] = d * (float)sc[s + 2] * (float)c1;
+      o[l + 64] = d * (float)sc[s + 4] * (float)c2;
+      o[l + 96] = d * (float)sc[s + 6] * (float)c3;
+    }
+  }
+}
+
+/* Dequantize `numel` elements of contiguous blocks.
+ * Follows the Q4_0/Q8_0/Q4_K/Q6_K cases of adapters/llama/gguf.c:650-967;
+ * other types return UNSUPPORTED (gguf.c:964-966). */
+int32_t orc_dequant(uint32_t type, const uint8_t *src, float *dst,
+                    uint64_t numel) {
+  if (src == NULL || dst == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  if (orc_type_bytes(type, numel) == 0u) {
+    return ORC_ERR_UNSUPPORTED;
+  }
+  switch (type) {
+  case ORC_Q4_0:
+    for (uint64_t b = 0; b < numel / 32u; ++b) dq_q4_0(src + 18u * b, dst + 32u * b);
+    break;
+  case ORC_Q8_0:
+    for (uint64_t b = 0; b < numel / 32u; ++b) dq_q8_0(src + 34u * b, dst + 32u * b);
+    break;
+  case ORC_Q4_K:
+    for (uint64_t b = 0; b < numel / 256u; ++b) dq_q4_k(src + 144u * b, dst + 256u * b);
+    break;
+  case ORC_Q6_K:
+    for (uint64_t b = 0; b < numel / 256u; ++b) dq_q6_k(src + 210u * b, dst + 256u * b);
+    break;
+  default:
+    return ORC_ERR_UNSUPPORTED;
+  }
+  return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Matmuls                                                                  */
+/* ---------------------------------------------------------------------- */
+
+/* c[i][j] = sum_{l<k} a[i][l] * b[l][j], one f32 accumulator per output,
+ * l ascending, no contraction (built with -ffp-contract=off).
+ * Follows cpu/reference/ref_ops.c:427-444 including its argument checks. */
+int32_t orc_gemm_seq_f32(uint64_t m, uint64_t n, uint64_t k, const float *a,
+                         const float *b, float *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || b == NULL || c == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (uint64_t l = 0; l < k; ++l) {
+        acc += a[i * k + l] * b[l * n + j];
+      }
+      c[i * n + j] = acc;
+    }
+  }
+  return ORC_OK;
+}
+
+static int32_t dequant_matrix(uint32_t type, uint64_t n, uint64_t k,
+                              const uint8_t *blocks, float **out) {
+  const uint64_t row_bytes = orc_type_bytes(type, k);
+  if (row_bytes == 0u) {
+    return ORC_ERR_UNSUPPORTED;
+  }
+  float *w = (float *)malloc((size_t)(n * k) * sizeof(float));
+  if (w == NULL) {
+    return ORC_ERR_NOMEM;
+  }
+  for (uint64_t r = 0; r < n; ++r) {
+    int32_t st = orc_dequant(type, blocks + r * row_bytes, w + r * k, k);
+    if (st != ORC_OK) {
+      free(w);
+      return st;
+    }
+  }
+  *out = w;
+  return ORC_OK;
+}
+
+/* The reference's CPU operator for one projection, as a composition:
+ * dequantize the native [N][K] blocks (adapters/llama/gguf.c:969-1012),
+ * transpose to [K][N] (adapters/llama/llama.c:196-209, used at :433),
+ * then pai_ref_gemm_f32 (cpu/reference/ref_ops.c:427-444) with a = x[M][K].
+ * The transpose is folded into the index: b[l][j] == W[j][l]. */
+int32_t orc_qgemm_seq_f32(uint32_t type, uint64_t n, uint64_t k,
+                          const uint8_t *blocks, uint64_t m, const float *x,
+                          float *y) {
+  if (m == 0u || n == 0u || k == 0u || blocks == NULL || x == NULL || y == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  float *w = NULL;
+  int32_t st = dequant_matrix(type, n, k, blocks, &w);
+  if (st != ORC_OK) {
+    return st;
+  }
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (uint64_t l = 0; l < k; ++l) {
+        acc += x[i * k + l] * w[j * k + l];
+      }
+      y[i * n + j] = acc;
+    }
+  }
+  free(w);
+  return ORC_OK;
+}
+
+/* Same composition with an f64 accumulator (the tolerance anchor). */
+int32_t orc_qgemm_f64(uint32_t type, uint64_t n, uint64_t k,
+                      const uint8_t *blocks, uint64_t m, const float *x,
+                      double *y) {
+  if (m == 0u || n == 0u || k == 0u || blocks == NULL || x == NULL || y == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  float *w = NULL;
+  int32_t st = dequant_matrix(type, n, k, blocks, &w);
+  if (st != ORC_OK) {
+    return st;
+  }
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      double acc = 0.0;
+      for (uint64_t l = 0; l < k; ++l) {
+        acc += (double)x[i * k + l] * (double)w[j * k + l];
+      }
+      y[i * n + j] = acc;
+    }
+  }
+  free(w);
+  return ORC_OK;
+}
+
+/* |a-b| <= max(abs_tol, |b|*rel_tol) per element; first failing index.
+ * Follows cpu/reference/ref_ops.c:518-541. */
+int32_t orc_compare_f32(const float *a, const float *b, uint64_t n,
+                        float abs_tol, float rel_tol, uint64_t *first_bad) {
+  if (first_bad != NULL) {
+    *first_bad = UINT64_MAX;
+  }
+  if ((a == NULL || b == NULL) && n != 0u) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    const float diff = fabsf(a[i] - b[i]);
+    const float rel = fabsf(b[i]) * rel_tol;
+    if (diff > (abs_tol > rel ? abs_tol : rel)) {
+      if (first_bad != NULL) {
+        *first_bad = i;
+      }
+      return ORC_ERR_MISMATCH;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* AVX2+FMA restatements (the CPU baseline)                                 */
+/* ---------------------------------------------------------------------- */
+
+#define ORC_AVX2 __attribute__((target("avx2,fma")))
+
+/* Horizontal sum of 8 lanes: high half onto low half, then the [1,0,3,2]
+ * and [2,3,0,1] shuffles. Follows cpu/optimized/opt_ops.c:89-99. */
+ORC_AVX2 static inline float hsum8(__m256 v) {
+  __m128 s = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+  s = _mm_add_ps(s, _mm_shuffle_ps(s, s, 0x4E));
+  s = _mm_add_ps(s, _mm_shuffle_ps(s, s, 0xB1));
+  return _mm_cvtss_f32(s);
+}
+
+/* y[i] = A[i][:] . x, A row-major [m][k]: one 8-wide FMA accumulator per
+ * row, horizontal sum, then a scalar tail.
+ * Follows cpu/optimized/opt_ops.c:527-550. */
+ORC_AVX2 int32_t orc_opt_gemv_avx2(uint64_t m, uint64_t k, const float *a,
+                                   const float *x, float *y) {
+  if (m == 0u || k == 0u || a == NULL || x == NULL || y == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t i = 0; i < m; ++i) {
+    const float *row = a + i * k;
+    __m256 acc = _mm256_setzero_ps();
+    uint64_t l = 0;
+    for (; l + 8u <= k; l += 8u) {
+      acc = _mm256_fmadd_ps(_mm256_loadu_ps(row + l), _mm256_loadu_ps(x + l), acc);
+    }
+    float s = hsum8(acc);
+    for (; l < k; ++l) {
+      s += row[l] * x[l];
+    }
+    y[i] = s;
+  }
+  return ORC_OK;
+}
+
+typedef struct {
+  uint64_t r0, r1, k;
+  const float *a, *x;
+  float *y;
+} gemv_part_t;
+
+static void *gemv_part(void *arg) {
+  gemv_part_t *p = (gemv_part_t *)arg;
+  if (p->r1 > p->r0) {
+    orc_opt_gemv_avx2(p->r1 - p->r0, p->k, p->a + p->r0 * p->k, p->x, p->y + p->r0);
+  }
+  return NULL;
+}
+
+/* Harness-parallel wrapper: contiguous row ranges of the single-thread
+ * kernel above on `threads` pthreads (the reference itself is serial). */
+int32_t orc_opt_gemv_avx2_mt(uint64_t m, uint64_t k, const float *a,
+                             const float *x, float *y, int threads) {
+  if (threads <= 1) {
+    return orc_opt_gemv_avx2(m, k, a, x, y);
+  }
+  if (m == 0u || k == 0u || a == NULL || x == NULL || y == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  if (threads > 256) {
+    threads = 256;
+  }
+  pthread_t tid[256];
+  gemv_part_t part[256];
+  for (int t = 0; t < threads; ++t) {
+    part[t].r0 = m * (uint64_t)t / (uint64_t)threads;
+    part[t].r1 = m * (uint64_t)(t + 1) / (uint64_t)threads;
+    part[t].k = k;
+    part[t].a = a;
+    part[t].x = x;
+    part[t].y = y;
+    if (pthread_create(&tid[t], NULL, gemv_part, &part[t]) != 0) {
+      gemv_part(&part[t]);
+      tid[t] = 0;
+    }
+  }
+  for (int t = 0; t < threads; ++t) {
+    if (tid[t] != 0) {
+      pthread_join(tid[t], NULL);
+    }
+  }
+  return ORC_OK;
+}
+
+/* c = a[m][k] * b[k][n]: 8 output columns per FMA accumulator, scalar
+ * tail columns. Follows cpu/optimized/opt_ops.c:497-525. */
+ORC_AVX2 int32_t orc_opt_gemm_avx2(uint64_t m, uint64_t n, uint64_t k,
+                                   const float *a, const float *b, float *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || b == NULL || c == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t i = 0; i < m; ++i) {
+    const float *ar = a + i * k;
+    float *cr = c + i * n;
+    uint64_t j = 0;
+    for (; j + 8u <= n; j += 8u) {
+      __m256 acc = _mm256_setzero_ps();
+      for (uint64_t l = 0; l < k; ++l) {
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(ar[l]), _mm256_loadu_ps(b + l * n + j), acc);
+      }
+      _mm256_storeu_ps(cr + j, acc);
+    }
+    for (; j < n; ++j) {
+      float s = 0.0f;
+      for (uint64_t l = 0; l < k; ++l) {
+        s += ar[l] * b[l * n + j];
+      }
+      cr[j] = s;
+    }
+  }
+  return ORC_OK;
+}
+
+/* W8 GEMM: int8 w_q[k][n] with f32 scales per (group of k-rows, column);
+ * group_size 0 or > k means one group. 8-column tiles, per-group scale
+ * vector, fmadd(a[t], cvt(w)*scale, acc).
+ * Follows cpu/optimized/opt_ops.c:552-592. */
+ORC_AVX2 int32_t orc_opt_gemm_w8_avx2(uint64_t m, uint64_t n, uint64_t k,
+                                      const float *a, const int8_t *w_q,
+                                      const float *b_scales,
+                                      uint64_t group_size, float *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || w_q == NULL ||
+      b_scales == NULL || c == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  const uint64_t gs = (group_size == 0u || group_size > k) ? k : group_size;
+  for (uint64_t i = 0; i < m; ++i) {
+    const float *ar = a + i * k;
+    float *cr = c + i * n;
+    uint64_t j = 0;
+    for (; j + 8u <= n; j += 8u) {
+      __m256 acc = _mm256_setzero_ps();
+      for (uint64_t g0 = 0; g0 < k; g0 += gs) {
+        const uint64_t g1 = g0 + gs < k ? g0 + gs : k;
+        const __m256 sv = _mm256_loadu_ps(b_scales + (g0 / gs) * n + j);
+        for (uint64_t t = g0; t < g1; ++t) {
+          const __m128i w8 = _mm_loadl_epi64((const __m128i *)(const void *)(w_q + t * n + j));
+          const __m256 wf = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(w8));
+          acc = _mm256_fmadd_ps(_mm256_set1_ps(ar[t]), _mm256_mul_ps(wf, sv), acc);
+        }
+      }
+      _mm256_storeu_ps(cr + j, acc);
+    }
+    for (; j < n; ++j) {
+      float s = 0.0f;
+      for (uint64_t t = 0; t < k; ++t) {
+        s += ar[t] * (float)w_q[t * n + j] * b_scales[(t / gs) * n + j];
+      }
+      cr[j] = s;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Textbook encoders (llama.cpp ggml-quants.c reference quantizers)         */
+/* ---------------------------------------------------------------------- */
+
+/* Q8_0: d = max|x|/127, q = round(x/d) (round half away from zero), d
+ * stored as f16. Published llama.cpp quantize_row_q8_0_ref algorithm. */
+void orc_q8_0_encode_ref(const float *x, uint8_t *out, uint64_t numel) {
+  for (uint64_t b = 0; b < numel / 32u; ++b) {
+    const float *v = x + 32u * b;
+    uint8_t *o = out + 34u * b;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      amax = fmaxf(amax, fabsf(v[j]));
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f32_to_f16_rne(d);
+    o[0] = (uint8_t)(dh & 0xFF);
+    o[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 32; ++j) {
+      o[2 + j] = (uint8_t)(int8_t)roundf(v[j] * id);
+    }
+  }
+}
+
+/* Q4_0: the signed value of largest magnitude m gives d = m / -8;
+ * code = min(15, (int8)(x/d + 8.5)). Published llama.cpp
+ * quantize_row_q4_0_ref algorithm. */
+void orc_q4_0_encode_ref(const float *x, uint8_t *out, uint64_t numel) {
+  for (uint64_t b = 0; b < numel / 32u; ++b) {
+    const float *v = x + 32u * b;
+    uint8_t *o = out + 18u * b;
+    float amax = 0.0f, mx = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      if (fabsf(v[j]) > amax) {
+        amax = fabsf(v[j]);
+        mx = v[j];
+      }
+    }
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint16_t dh = f32_to_f16_rne(d);
+    o[0] = (uint8_t)(dh & 0xFF);
+    o[1] = (uint8_t)(dh >> 8);
+    for (int j = 0; j < 16; ++j) {
+      int c0 = (int)(int8_t)(v[j] * id + 8.5f);
+      int c1 = (int)(int8_t)(v[j + 16] * id + 8.5f);
+      c0 = c0 < 15 ? c0 : 15;
+      c1 = c1 < 15 ? c1 : 15;
+      o[2 + j] = (uint8_t)(c0 | (c1 << 4));
+    }
+  }
+}

@@ -1,0 +1,93 @@
+/*
+ * CPU oracle for the quantized-weights matmul (test infrastructure only).
+ *
+ * This library is the checker, never the product: only the test suite,
+ * the smoke check and the benchmark's CPU-baseline leg load it. It
+ * restates, function by function, the reference's block dequantization
+ * (adapters/llama/gguf.c), its scalar f32 GEMM (cpu/reference/ref_ops.c)
+ * and its AVX2+FMA kernels (cpu/optimized/opt_ops.c). Each function cites
+ * the reference lines it follows.
+ *
+ * Parity pins (what checks each function independently of its own text):
+ *   orc_f16_to_f32        exhaustive 65536-pattern check against
+ *                         numpy float16->float32, plus the reference's
+ *                         literals (tests/test_gguf.c:270-276).
+ *   orc_scale_min_k4      brute force against a bit-level closed form
+ *                         (6-bit fields of a 96-bit little-endian word).
+ *   orc_dequant           the reference's hand vectors
+ *                         (tests/test_gguf.c:284-298, 317-332, 451-491,
+ *                         519-538), invariants (zero block, linearity in
+ *                         d, dmin=0 reduction, one-hot codes), and the
+ *                         reference's own gguf.c built into oracle/_ref.
+ *   orc_gemm_seq_f32      brute-force f64 sums on tiny shapes, one-hot
+ *                         activations, and the reference's ref_ops.c
+ *                         built into oracle/_ref (bit-exact).
+ *   orc_qgemm_seq_f32     composition of the two above; one-hot x returns
+ *                         a dequantized column exactly.
+ *   orc_qgemm_f64         closed-form sums on tiny shapes.
+ *   orc_opt_gemv_avx2 /   the reference's opt_ops.c built into oracle/_ref
+ *   orc_opt_gemm_w8_avx2  (bit-exact), and tolerance vs the f64 oracle.
+ *   orc_q8_0_encode_ref / textbook llama.cpp encoders used to pin the
+ *   orc_q4_0_encode_ref   product encoders; the reference has no encoder,
+ *                         so these two are pinned only by round-trip
+ *                         bounds and by brute-force optimality checks.
+ */
+#ifndef PAI_ORACLE_H
+#define PAI_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, as in adapters/llama/gguf.h:34-51. */
+#define ORC_Q4_0 2u
+#define ORC_Q8_0 8u
+#define ORC_Q4_K 12u
+#define ORC_Q6_K 14u
+
+/* Status codes, as in sdk/include/pai/error.h:13-23. */
+#define ORC_OK 0
+#define ORC_ERR_INVALID_ARG -1
+#define ORC_ERR_NOMEM -2
+#define ORC_ERR_UNSUPPORTED -3
+#define ORC_ERR_MISMATCH -6
+
+float orc_f16_to_f32(uint16_t h);
+void orc_f16_to_f32_bits(const uint16_t *h, uint32_t *out, uint64_t n);
+void orc_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *mn);
+uint64_t orc_type_bytes(uint32_t type, uint64_t numel);
+int32_t orc_dequant(uint32_t type, const uint8_t *src, float *dst,
+                    uint64_t numel);
+
+int32_t orc_gemm_seq_f32(uint64_t m, uint64_t n, uint64_t k, const float *a,
+                         const float *b, float *c);
+int32_t orc_qgemm_seq_f32(uint32_t type, uint64_t n, uint64_t k,
+                          const uint8_t *blocks, uint64_t m, const float *x,
+                          float *y);
+int32_t orc_qgemm_f64(uint32_t type, uint64_t n, uint64_t k,
+                      const uint8_t *blocks, uint64_t m, const float *x,
+                      double *y);
+int32_t orc_compare_f32(const float *a, const float *b, uint64_t n,
+                        float abs_tol, float rel_tol, uint64_t *first_bad);
+
+int32_t orc_opt_gemv_avx2(uint64_t m, uint64_t k, const float *a,
+                          const float *x, float *y);
+int32_t orc_opt_gemv_avx2_mt(uint64_t m, uint64_t k, const float *a,
+                             const float *x, float *y, int threads);
+int32_t orc_opt_gemm_avx2(uint64_t m, uint64_t n, uint64_t k, const float *a,
+                          const float *b, float *c);
+int32_t orc_opt_gemm_w8_avx2(uint64_t m, uint64_t n, uint64_t k,
+                             const float *a, const int8_t *w_q,
+                             const float *b_scales, uint64_t group_size,
+                             float *c);
+
+void orc_q8_0_encode_ref(const float *x, uint8_t *out, uint64_t numel);
+void orc_q4_0_encode_ref(const float *x, uint8_t *out, uint64_t numel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAI_ORACLE_H */

@@ -1,0 +1,432 @@
+/*
+ * pai_hip host layer (C11): device bring-up, packed-matrix handles,
+ * argument validation, dispatch to the gfx950 kernels and HIP-error to
+ * pai_status_t mapping. See include/pai_hip.h for the contract.
+ *
+ * No CPU fallback exists: without a usable gfx950 device every compute
+ * entry point returns PAI_ERR_INIT.
+ */
+#define _GNU_SOURCE
+#include "pai_hip.h"
+
+#include <hip/hip_runtime_api.h>
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "paik.h"
+
+struct pai_qmat {
+  uint32_t type;
+  uint64_t n, k;
+  uint64_t packed_bytes; /* N * type_bytes(K) */
+  void *dev;             /* one allocation holding every plane */
+  uint64_t dev_bytes;
+  int device;
+  paik_qview_t view;
+};
+
+/* ---------------------------------------------------------------------- */
+/* Errors                                                                   */
+/* ---------------------------------------------------------------------- */
+
+static _Thread_local char t_err[256];
+
+static pai_status_t fail(pai_status_t st, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(t_err, sizeof t_err, fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+const char *pai_hip_last_error(void) { return t_err; }
+
+/* hipError_t -> pai_status_t (sdk/include/pai/error.h codes). */
+static pai_status_t map_hip(hipError_t e, const char *what) {
+  pai_status_t st;
+  switch (e) {
+  case hipSuccess:
+    return PAI_OK;
+  case hipErrorOutOfMemory:
+    st = PAI_ERR_NOMEM;
+    break;
+  case hipErrorNoDevice:
+  case hipErrorInvalidDevice:
+  case hipErrorNotInitialized:
+  case hipErrorInsufficientDriver:
+  case hipErrorNoBinaryForGpu:
+    st = PAI_ERR_INIT;
+    break;
+  case hipErrorLaunchTimeOut:
+    st = PAI_ERR_TIMEOUT;
+    break;
+  default:
+    st = PAI_ERR_INTERNAL;
+    break;
+  }
+  return fail(st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(call, what)                                                    \
+  do {                                                                         \
+    hipError_t e_ = (call);                                                    \
+    if (e_ != hipSuccess) return map_hip(e_, what);                            \
+  } while (0)
+
+/* ---------------------------------------------------------------------- */
+/* Lifecycle                                                                */
+/* ---------------------------------------------------------------------- */
+
+static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
+static int g_ready;
+static int g_device;
+
+/* Host-pointer staging (grow-only), guarded by g_stage_lock. */
+static pthread_mutex_t g_stage_lock = PTHREAD_MUTEX_INITIALIZER;
+static void *g_stage;
+static uint64_t g_stage_bytes;
+
+pai_status_t pai_hip_init(void) {
+  pthread_mutex_lock(&g_lock);
+  if (g_ready) {
+    pthread_mutex_unlock(&g_lock);
+    return PAI_OK;
+  }
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0) {
+    pthread_mutex_unlock(&g_lock);
+    return fail(PAI_ERR_INIT, "no HIP device (%s)", hipGetErrorString(e));
+  }
+  int dev = 0;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    pthread_mutex_unlock(&g_lock);
+    return map_hip(e, "hipGetDevice");
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    pthread_mutex_unlock(&g_lock);
+    return map_hip(e, "hipGetDeviceProperties");
+  }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    pthread_mutex_unlock(&g_lock);
+    return fail(PAI_ERR_INIT, "device %d is %s; kernels are built for gfx950", dev,
+                prop.gcnArchName);
+  }
+  g_device = dev;
+  g_ready = 1;
+  pthread_mutex_unlock(&g_lock);
+  return PAI_OK;
+}
+
+pai_status_t pai_hip_shutdown(void) {
+  pthread_mutex_lock(&g_stage_lock);
+  if (g_stage != NULL) {
+    (void)hipFree(g_stage);
+    g_stage = NULL;
+    g_stage_bytes = 0;
+  }
+  pthread_mutex_unlock(&g_stage_lock);
+  pthread_mutex_lock(&g_lock);
+  g_ready = 0;
+  pthread_mutex_unlock(&g_lock);
+  return PAI_OK;
+}
+
+static pai_status_t ensure_ready(void) {
+  if (g_ready) return PAI_OK;
+  return pai_hip_init();
+}
+
+/* ---------------------------------------------------------------------- */
+/* Formats and layout                                                       */
+/* ---------------------------------------------------------------------- */
+
+static uint64_t block_elems(uint32_t type) {
+  switch (type) {
+  case PAI_QTYPE_Q4_0:
+  case PAI_QTYPE_Q8_0:
+    return 32u;
+  case PAI_QTYPE_Q4_K:
+  case PAI_QTYPE_Q6_K:
+    return 256u;
+  default:
+    return 0u;
+  }
+}
+
+static uint64_t block_bytes(uint32_t type) {
+  switch (type) {
+  case PAI_QTYPE_Q4_0: return 18u;
+  case PAI_QTYPE_Q8_0: return 34u;
+  case PAI_QTYPE_Q4_K: return 144u;
+  case PAI_QTYPE_Q6_K: return 210u;
+  default: return 0u;
+  }
+}
+
+/* adapters/llama/gguf.c:562-597 semantics for the four supported types. */
+uint64_t pai_qtype_bytes(uint32_t type, uint64_t numel) {
+  const uint64_t qk = block_elems(type);
+  if (qk == 0u || numel % qk != 0u) return 0u;
+  return numel / qk * block_bytes(type);
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255u) & ~(uint64_t)255u; }
+
+uint64_t paik_plan_layout(uint32_t type, uint64_t n, uint64_t k, uint64_t *off_q,
+                          uint64_t *off_aux, uint64_t *off_meta, uint64_t *off_d) {
+  const uint64_t qk = block_elems(type);
+  if (qk == 0u || n == 0u || k == 0u || k % qk != 0u) return 0u;
+  const uint64_t nb = k / qk;
+  uint64_t q_bytes = 0, aux_bytes = 0, meta_bytes = 0, d_bytes = 0;
+  switch (type) {
+  case PAI_QTYPE_Q8_0: q_bytes = n * k; d_bytes = n * nb * 2u; break;
+  case PAI_QTYPE_Q4_0: q_bytes = n * k / 2u; d_bytes = n * nb * 2u; break;
+  case PAI_QTYPE_Q4_K: q_bytes = n * k / 2u; meta_bytes = n * nb * 16u; break;
+  case PAI_QTYPE_Q6_K:
+    q_bytes = n * k / 2u;
+    aux_bytes = n * k / 4u;
+    meta_bytes = n * nb * 16u;
+    d_bytes = n * nb * 2u;
+    break;
+  default: return 0u;
+  }
+  uint64_t off = 0;
+  *off_q = off;
+  off = align256(off + q_bytes);
+  *off_aux = off;
+  off = align256(off + aux_bytes);
+  *off_meta = off;
+  off = align256(off + meta_bytes);
+  *off_d = off;
+  off = align256(off + d_bytes);
+  return off;
+}
+
+/* Kernel index math is 32-bit in rows/columns; byte offsets are 64-bit. */
+#define PAI_MAX_DIM ((uint64_t)1 << 30)
+
+static pai_status_t check_shape(uint32_t type, uint64_t n, uint64_t k) {
+  if (n == 0u || k == 0u) return fail(PAI_ERR_INVALID_ARG, "zero dimension");
+  if (block_elems(type) == 0u) return fail(PAI_ERR_UNSUPPORTED, "ggml type %u not supported", type);
+  if (k % block_elems(type) != 0u)
+    return fail(PAI_ERR_UNSUPPORTED, "K=%llu is not a whole number of %llu-element blocks",
+                (unsigned long long)k, (unsigned long long)block_elems(type));
+  if (n > PAI_MAX_DIM || k > PAI_MAX_DIM) return fail(PAI_ERR_UNSUPPORTED, "dimension above 2^30");
+  return PAI_OK;
+}
+
+static pai_status_t make_qmat(pai_qmat_t **out, uint32_t type, uint64_t n, uint64_t k,
+                              const void *dev_native, void *stream) {
+  uint64_t oq, oa, om, od;
+  const uint64_t bytes = paik_plan_layout(type, n, k, &oq, &oa, &om, &od);
+  pai_qmat_t *w = (pai_qmat_t *)calloc(1, sizeof *w);
+  if (w == NULL) return fail(PAI_ERR_NOMEM, "host allocation");
+  hipError_t e = hipMalloc(&w->dev, bytes);
+  if (e != hipSuccess) {
+    free(w);
+    return map_hip(e, "hipMalloc(weights)");
+  }
+  w->type = type;
+  w->n = n;
+  w->k = k;
+  w->packed_bytes = n * pai_qtype_bytes(type, k);
+  w->dev_bytes = bytes;
+  w->device = g_device;
+  uint8_t *base = (uint8_t *)w->dev;
+  w->view.q = base + oq;
+  w->view.aux = base + oa;
+  w->view.meta = base + om;
+  w->view.d = (const uint16_t *)(base + od);
+  w->view.type = type;
+  w->view.n = (uint32_t)n;
+  w->view.k = (uint32_t)k;
+  w->view.nb = (uint32_t)(k / block_elems(type));
+  w->view.q_stride = (uint32_t)(type == PAI_QTYPE_Q8_0 ? k : k / 2u);
+  int le = paik_repack(&w->view, (const uint8_t *)dev_native, stream);
+  if (le == 0) le = (int)hipStreamSynchronize((hipStream_t)stream);
+  if (le != 0) {
+    (void)hipFree(w->dev);
+    free(w);
+    return map_hip((hipError_t)le, "repack");
+  }
+  *out = w;
+  return PAI_OK;
+}
+
+pai_status_t pai_qmat_upload(pai_qmat_t **out, uint32_t type, uint64_t n, uint64_t k,
+                             const void *blocks, uint64_t nbytes) {
+  if (out == NULL || blocks == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  *out = NULL;
+  pai_status_t st = check_shape(type, n, k);
+  if (st != PAI_OK) return st;
+  if (nbytes != n * pai_qtype_bytes(type, k))
+    return fail(PAI_ERR_MISMATCH, "nbytes=%llu, expected %llu", (unsigned long long)nbytes,
+                (unsigned long long)(n * pai_qtype_bytes(type, k)));
+  st = ensure_ready();
+  if (st != PAI_OK) return st;
+  void *staging = NULL;
+  HIP_TRY(hipMalloc(&staging, nbytes), "hipMalloc(staging)");
+  hipError_t e = hipMemcpy(staging, blocks, nbytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(staging);
+    return map_hip(e, "hipMemcpy(blocks)");
+  }
+  st = make_qmat(out, type, n, k, staging, NULL);
+  (void)hipFree(staging);
+  return st;
+}
+
+pai_status_t pai_qmat_upload_device(pai_qmat_t **out, uint32_t type, uint64_t n, uint64_t k,
+                                    const void *dev_blocks, uint64_t nbytes, void *stream) {
+  if (out == NULL || dev_blocks == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  *out = NULL;
+  pai_status_t st = check_shape(type, n, k);
+  if (st != PAI_OK) return st;
+  if (nbytes != n * pai_qtype_bytes(type, k))
+    return fail(PAI_ERR_MISMATCH, "nbytes=%llu, expected %llu", (unsigned long long)nbytes,
+                (unsigned long long)(n * pai_qtype_bytes(type, k)));
+  st = ensure_ready();
+  if (st != PAI_OK) return st;
+  return make_qmat(out, type, n, k, dev_blocks, stream);
+}
+
+pai_status_t pai_qmat_free(pai_qmat_t *w) {
+  if (w == NULL) return PAI_OK;
+  hipError_t e = hipFree(w->dev);
+  free(w);
+  return e == hipSuccess ? PAI_OK : map_hip(e, "hipFree(weights)");
+}
+
+pai_status_t pai_qmat_shape(const pai_qmat_t *w, uint32_t *type, uint64_t *n, uint64_t *k) {
+  if (w == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL handle");
+  if (type != NULL) *type = w->type;
+  if (n != NULL) *n = w->n;
+  if (k != NULL) *k = w->k;
+  return PAI_OK;
+}
+
+uint64_t pai_qmat_bytes(const pai_qmat_t *w) { return w != NULL ? w->packed_bytes : 0u; }
+
+/* ---------------------------------------------------------------------- */
+/* Compute                                                                  */
+/* ---------------------------------------------------------------------- */
+
+#define PAI_MFMA_MIN_M 32u
+
+static pai_status_t launch(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
+                           uint32_t flags, hipStream_t s) {
+  int e;
+  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
+    e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
+  } else {
+    e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, (flags & PAI_QGEMM_MFMA_BF16) != 0u, s);
+  }
+  return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+}
+
+static pai_status_t check_call(const pai_qmat_t *w, uint64_t m, const void *x, const void *y) {
+  if (w == NULL || x == NULL || y == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  if (m == 0u) return fail(PAI_ERR_INVALID_ARG, "m == 0");
+  if (m > PAI_MAX_DIM) return fail(PAI_ERR_UNSUPPORTED, "m above 2^30");
+  return ensure_ready();
+}
+
+pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
+                                 uint32_t flags, void *stream) {
+  pai_status_t st = check_call(w, m, x, y);
+  if (st != PAI_OK) return st;
+  if (((uintptr_t)x & 15u) != 0u || ((uintptr_t)y & 3u) != 0u)
+    return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned, y 4-byte aligned");
+  return launch(w, m, x, y, flags, (hipStream_t)stream);
+}
+
+pai_status_t pai_qgemm_f32(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
+                           uint32_t flags) {
+  pai_status_t st = check_call(w, m, x, y);
+  if (st != PAI_OK) return st;
+  if ((flags & PAI_QGEMM_DEVICE_PTRS) != 0u) {
+    st = pai_qgemm_f32_async(w, m, x, y, flags, NULL);
+    if (st != PAI_OK) return st;
+    HIP_TRY(hipStreamSynchronize(NULL), "qgemm");
+    return PAI_OK;
+  }
+  const uint64_t xb = align256(m * w->k * sizeof(float));
+  const uint64_t yb = align256(m * w->n * sizeof(float));
+  pthread_mutex_lock(&g_stage_lock);
+  if (g_stage_bytes < xb + yb) {
+    if (g_stage != NULL) (void)hipFree(g_stage);
+    g_stage = NULL;
+    g_stage_bytes = 0;
+    hipError_t e = hipMalloc(&g_stage, xb + yb);
+    if (e != hipSuccess) {
+      pthread_mutex_unlock(&g_stage_lock);
+      return map_hip(e, "hipMalloc(x/y staging)");
+    }
+    g_stage_bytes = xb + yb;
+  }
+  float *dx = (float *)g_stage;
+  float *dy = (float *)((uint8_t *)g_stage + xb);
+  hipError_t e = hipMemcpy(dx, x, m * w->k * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    st = launch(w, m, dx, dy, flags, NULL);
+    if (st == PAI_OK) {
+      e = hipMemcpy(y, dy, m * w->n * sizeof(float), hipMemcpyDeviceToHost);
+      if (e != hipSuccess) st = map_hip(e, "hipMemcpy(y)");
+    }
+  } else {
+    st = map_hip(e, "hipMemcpy(x)");
+  }
+  pthread_mutex_unlock(&g_stage_lock);
+  return st;
+}
+
+pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags) {
+  if (w == NULL || out == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  pai_status_t st = ensure_ready();
+  if (st != PAI_OK) return st;
+  const uint64_t bytes = w->n * w->k * sizeof(float);
+  float *dst = out;
+  if ((flags & PAI_QGEMM_DEVICE_PTRS) == 0u) {
+    HIP_TRY(hipMalloc((void **)&dst, bytes), "hipMalloc(dequant out)");
+  } else if (((uintptr_t)out & 15u) != 0u) {
+    return fail(PAI_ERR_INVALID_ARG, "out must be 16-byte aligned");
+  }
+  int le = paik_dequant(&w->view, dst, NULL);
+  if (le == 0) le = (int)hipStreamSynchronize(NULL);
+  if (le == 0 && dst != out) le = (int)hipMemcpy(out, dst, bytes, hipMemcpyDeviceToHost);
+  if (dst != out) (void)hipFree(dst);
+  return le == 0 ? PAI_OK : map_hip((hipError_t)le, "dequant");
+}
+
+/* ---------------------------------------------------------------------- */
+/* Registry descriptors                                                     */
+/* ---------------------------------------------------------------------- */
+
+static const pai_hip_op_descriptor_t k_ops[] = {
+    {"qgemm_q4_0_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
+    {"qgemm_q8_0_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
+    {"qgemm_q4_k_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
+    {"qgemm_q6_k_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
+};
+
+const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count) {
+  if (count != NULL) *count = (uint32_t)(sizeof k_ops / sizeof k_ops[0]);
+  return k_ops;
+}
+
+const char *pai_hip_op_name(uint32_t type) {
+  switch (type) {
+  case PAI_QTYPE_Q4_0: return k_ops[0].name;
+  case PAI_QTYPE_Q8_0: return k_ops[1].name;
+  case PAI_QTYPE_Q4_K: return k_ops[2].name;
+  case PAI_QTYPE_Q6_K: return k_ops[3].name;
+  default: return NULL;
+  }
+}

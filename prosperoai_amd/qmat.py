@@ -1,0 +1,112 @@
+"""Python view of the C-ABI for tests and benchmarks.
+
+Mirrors the reference's operator contract: the C entry points return
+pai_status_t and never allocate the caller's buffers; here a non-zero status
+raises PaiError carrying the status name and the library's message.
+torch tensors (device memory, streams) are plumbing only; every kernel runs
+through libpai_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import HipDescriptor, check, lib
+
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+QTYPES = {"q4_0": Q4_0, "q8_0": Q8_0, "q4_k": Q4_K, "q6_k": Q6_K}
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+
+FLAG_DEVICE_PTRS = 1 << 0
+FLAG_MFMA_BF16 = 1 << 1
+FLAG_FP32 = 1 << 2
+MFMA_MIN_M = 32
+
+
+def qtype_bytes(qtype: int, numel: int) -> int:
+    return int(lib().pai_qtype_bytes(qtype, numel))
+
+
+def normal_f32(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().paiq_normal_f32(seed & 0xFFFFFFFFFFFFFFFF, mean, std, out.ctypes.data, n)
+    return out
+
+
+def quantize(qtype: int, w: np.ndarray, threads: int = 0) -> np.ndarray:
+    """Encode f32 rows [N][K] into native GGUF blocks (uint8 [N][row_bytes])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    rb = qtype_bytes(qtype, k)
+    out = np.empty((n, rb), dtype=np.uint8)
+    check(lib().paiq_quantize(qtype, w.ctypes.data, n, k, out.ctypes.data, out.nbytes, threads),
+          "paiq_quantize")
+    return out
+
+
+def init() -> None:
+    check(lib().pai_hip_init(), "pai_hip_init")
+
+
+def descriptors() -> list[HipDescriptor]:
+    count = C.c_uint32(0)
+    ptr = lib().pai_hip_op_descriptors(C.byref(count))
+    arr = C.cast(ptr, C.POINTER(HipDescriptor))
+    return [arr[i] for i in range(count.value)]
+
+
+class QMat:
+    """A packed W[N][K] resident in device memory (pai_qmat_t)."""
+
+    def __init__(self, qtype: int, n: int, k: int, blocks, *, device_ptr: int | None = None,
+                 stream: int = 0):
+        self.qtype, self.n, self.k = qtype, n, k
+        self._h = C.c_void_p()
+        if device_ptr is not None:
+            nbytes = n * qtype_bytes(qtype, k)
+            check(lib().pai_qmat_upload_device(C.byref(self._h), qtype, n, k, device_ptr, nbytes,
+                                               stream or None), "pai_qmat_upload_device")
+        else:
+            b = np.ascontiguousarray(blocks, dtype=np.uint8)
+            check(lib().pai_qmat_upload(C.byref(self._h), qtype, n, k, b.ctypes.data, b.nbytes),
+                  "pai_qmat_upload")
+
+    @property
+    def handle(self) -> int:
+        return self._h.value
+
+    @property
+    def nbytes(self) -> int:
+        return int(lib().pai_qmat_bytes(self._h))
+
+    def free(self) -> None:
+        if self._h.value:
+            check(lib().pai_qmat_free(self._h), "pai_qmat_free")
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    # ---- host-pointer entry points (synchronous) ----
+    def gemm(self, x: np.ndarray, flags: int = 0) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        m = x.shape[0] if x.ndim == 2 else 1
+        y = np.empty((m, self.n), dtype=np.float32)
+        check(lib().pai_qgemm_f32(self._h, m, x.ctypes.data, y.ctypes.data, flags),
+              "pai_qgemm_f32")
+        return y
+
+    def dequant(self) -> np.ndarray:
+        out = np.empty((self.n, self.k), dtype=np.float32)
+        check(lib().pai_qdequant_f32(self._h, out.ctypes.data, 0), "pai_qdequant_f32")
+        return out
+
+    # ---- device-pointer entry points (torch tensors as plumbing) ----
+    def gemm_async(self, x_ptr: int, y_ptr: int, m: int, flags: int = 0, stream: int = 0) -> None:
+        check(lib().pai_qgemm_f32_async(self._h, m, x_ptr, y_ptr, flags | FLAG_DEVICE_PTRS,
+                                        stream or None), "pai_qgemm_f32_async")

@@ -1,0 +1,252 @@
+"""GPU parity: every kernel of libpai_hip.so against the CPU oracle, called
+through the C-ABI.
+
+Bars:
+  dequant                      bit-exact (NaN outputs compared as NaN)
+  M < 32 and PAI_QGEMM_FP32    rel-L2 <= 1e-5 vs the reference's sequential
+                               f32 operator (and vs the f64 oracle)
+  M >= 32 MFMA                 rel-L2 <= 2e-3 (fp16 operands), 1.6e-2 (bf16)
+                               vs the f64 oracle
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_bind as ob
+import prosperoai_amd as pa
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32, TOL_F16, TOL_BF16 = 1e-5, 2e-3, 1.6e-2
+QK = pa.BLOCK_ELEMS
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    say("[gpu] pai_hip_init")
+    pa.init()
+    yield
+
+
+def weights(qtype: int, n: int, k: int, seed: int) -> np.ndarray:
+    w = pa.normal_f32(seed, n * k, 0.0, 0.02).reshape(n, k)
+    return pa.quantize(qtype, w)
+
+
+def rel_l2(y: np.ndarray, ref: np.ndarray) -> float:
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(np.asarray(y, np.float64) - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+# ------------------------------------------------------------------ dequant
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("n,nblk", [(1, 1), (5, 3), (64, 16), (33, 7)])
+def test_dequant_bit_exact(qtype, n, nblk):
+    import make_golden
+    say(f"[gpu] dequant type={qtype} n={n} blocks/row={nblk}")
+    rng = np.random.default_rng(1000 * qtype + n + nblk)
+    k = nblk * QK[qtype]
+    raw = make_golden.random_blocks(rng, qtype, n * nblk).reshape(n, -1)
+    w = pa.QMat(qtype, n, k, raw)
+    got = w.dequant()
+    want = ob.dequant(qtype, raw, n * k).reshape(n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_every_f16_scale():
+    """Q8_0 rows whose scale runs over all 65536 f16 patterns."""
+    say("[gpu] dequant all f16 scales")
+    n = 65536
+    blk = np.zeros((n, 34), np.uint8)
+    h = np.arange(n, dtype=np.uint32)
+    blk[:, 0] = (h & 0xFF).astype(np.uint8)
+    blk[:, 1] = (h >> 8).astype(np.uint8)
+    codes = np.array([1, -1, 127, -128, 0, 2, 3, -7] * 4, np.int8)
+    blk[:, 2:] = codes.view(np.uint8)
+    got = pa.QMat(8, n, 32, blk).dequant()
+    want = ob.dequant(8, blk, n * 32).reshape(n, 32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_dequant_hand_vectors():
+    import json
+    from pathlib import Path
+    say("[gpu] dequant reference hand vectors")
+    d = json.loads((Path(__file__).parent / "golden" / "gguf_hand_vectors.json").read_text())
+    for c in d["cases"]:
+        raw = np.frombuffer(bytes.fromhex(c["raw"]), np.uint8)
+        got = pa.QMat(c["type"], 1, c["numel"], raw).dequant()[0]
+        assert np.array_equal(got, np.asarray(c["expect"], np.float32)), c["name"]
+
+
+# ------------------------------------------------------------------ M = 1 GEMV
+SHAPES_M1 = [
+    (1, None), (7, None), (33, 3), (129, 9), (1000, 65), (64, 448),  # K in blocks
+]
+
+
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("n,kb", SHAPES_M1)
+def test_gemv_m1_parity(qtype, n, kb):
+    qk = QK[qtype]
+    k = qk * (kb if kb is not None else (1 if qk == 256 else 3))
+    say(f"[gpu] gemv M=1 type={qtype} n={n} k={k}")
+    blocks = weights(qtype, n, k, 7 * n + k + qtype)
+    x = pa.normal_f32(99 + k, k).reshape(1, k)
+    w = pa.QMat(qtype, n, k, blocks)
+    y = w.gemm(x)
+    ref = ob.qgemm_seq(qtype, n, k, blocks, x)
+    ref64 = ob.qgemm_f64(qtype, n, k, blocks, x)
+    assert rel_l2(y, ref) <= TOL_F32
+    assert rel_l2(y, ref64) <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+def test_gemv_one_hot_returns_exact_column(qtype):
+    n, k = 70, 4 * QK[qtype] if QK[qtype] == 256 else 2048 + 64
+    say(f"[gpu] gemv one-hot type={qtype}")
+    blocks = weights(qtype, n, k, 5 + qtype)
+    w = pa.QMat(qtype, n, k, blocks)
+    deq = ob.dequant(qtype, blocks, n * k).reshape(n, k)
+    for j in (0, 17, k // 2 + 5, k - 1):
+        x = np.zeros((1, k), np.float32)
+        x[0, j] = 1.0
+        assert np.array_equal(w.gemm(x)[0], deq[:, j])
+
+
+LLAMA8B = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+           "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+
+
+@pytest.mark.parametrize("qtype", [2, 12])
+@pytest.mark.parametrize("proj", ["k", "o", "gate", "down"])
+def test_gemv_llama8b_shapes(qtype, proj):
+    n, k = LLAMA8B[proj]
+    say(f"[gpu] gemv 8B shape type={qtype} proj={proj} n={n} k={k}")
+    blocks = weights(qtype, n, k, 0xC0DE0000 + 16 * 2 + list(LLAMA8B).index(proj))
+    x = pa.normal_f32(0x5A5A, k).reshape(1, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x)
+    assert rel_l2(y, ob.qgemm_seq(qtype, n, k, blocks, x)) <= TOL_F32
+
+
+def test_gemv_q8_0_config1_and_q6_k_down():
+    for qtype, (n, k) in ((8, (4096, 4096)), (14, (4096, 14336))):
+        say(f"[gpu] gemv type={qtype} n={n} k={k}")
+        blocks = weights(qtype, n, k, 0xC0DE0010 + qtype)
+        x = pa.normal_f32(0xC0DE0010 ^ 0x5A5A, k).reshape(1, k)
+        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        assert rel_l2(y, ob.qgemm_seq(qtype, n, k, blocks, x)) <= TOL_F32
+
+
+# ------------------------------------------------------------------ small batch
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 31])
+def test_small_batch_parity(qtype, m):
+    n, k = 300, 2 * QK[qtype] * (8 if QK[qtype] == 32 else 1)
+    say(f"[gpu] gemm M={m} type={qtype} n={n} k={k}")
+    blocks = weights(qtype, n, k, 31 * m + qtype)
+    x = pa.normal_f32(3 * m, m * k).reshape(m, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x)
+    ref = ob.qgemm_seq(qtype, n, k, blocks, x)
+    for i in range(m):
+        assert rel_l2(y[i], ref[i]) <= TOL_F32, i
+
+
+# ------------------------------------------------------------------ MFMA path
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("m", [32, 33, 64, 100])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_mfma_parity(qtype, m, bf16):
+    n, k = 200, 3 * 256
+    say(f"[gpu] gemm MFMA M={m} type={qtype} bf16={bf16} n={n} k={k}")
+    blocks = weights(qtype, n, k, 17 * m + qtype)
+    x = pa.normal_f32(5 * m + 1, m * k).reshape(m, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x, pa.FLAG_MFMA_BF16 if bf16 else 0)
+    ref64 = ob.qgemm_f64(qtype, n, k, blocks, x)
+    err = rel_l2(y, ref64)
+    assert err <= (TOL_BF16 if bf16 else TOL_F16), err
+    assert err > 0.0  # it really is the reduced-precision path
+
+
+def test_mfma_ragged_k_for_32_blocks():
+    """Q4_0/Q8_0 with K not a multiple of the 256-column tile."""
+    for qtype in (2, 8):
+        n, k, m = 77, 32 * 11, 40
+        say(f"[gpu] gemm MFMA ragged K type={qtype}")
+        blocks = weights(qtype, n, k, 3 + qtype)
+        x = pa.normal_f32(11, m * k).reshape(m, k)
+        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        assert rel_l2(y, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
+
+
+def test_fp32_flag_gives_reference_precision_at_large_m():
+    qtype, n, k, m = 12, 96, 512, 48
+    say("[gpu] gemm FP32 flag M=48")
+    blocks = weights(qtype, n, k, 77)
+    x = pa.normal_f32(78, m * k).reshape(m, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x, pa.FLAG_FP32)
+    ref = ob.qgemm_seq(qtype, n, k, blocks, x)
+    assert rel_l2(y, ref) <= TOL_F32
+
+
+def test_prefill_shape_gate_q4k_m512():
+    qtype, (n, k), m = 12, LLAMA8B["gate"], 512
+    say("[gpu] prefill gate M=512")
+    blocks = weights(qtype, n, k, 0xC0DE0040)
+    x = pa.normal_f32(0xC0DE0040 ^ 0x5A5A, m * k).reshape(m, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x)
+    rows = np.arange(0, m, 37)
+    ref = ob.qgemm_f64(qtype, n, k, blocks, x[rows])
+    assert rel_l2(y[rows], ref) <= TOL_F16
+
+
+# ------------------------------------------------------------------ device pointers
+def test_device_pointer_path_matches_host_path():
+    import torch
+    qtype, n, k = 12, 512, 2048
+    say("[gpu] device-pointer path")
+    blocks = weights(qtype, n, k, 4)
+    w = pa.QMat(qtype, n, k, blocks)
+    for m in (1, 3, 40):
+        x = pa.normal_f32(m, m * k).reshape(m, k)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        w.gemm_async(xd.data_ptr(), yd.data_ptr(), m, 0, stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(yd.cpu().numpy(), w.gemm(x))
+
+
+def test_upload_from_device_blocks():
+    import torch
+    qtype, n, k = 14, 40, 512
+    say("[gpu] upload from device")
+    blocks = weights(qtype, n, k, 8)
+    dev = torch.from_numpy(blocks.reshape(-1)).cuda()
+    w2 = pa.QMat(qtype, n, k, None, device_ptr=dev.data_ptr())
+    assert np.array_equal(w2.dequant(), pa.QMat(qtype, n, k, blocks).dequant())
+
+
+def test_gpu_argument_errors():
+    import torch
+    say("[gpu] argument errors")
+    lib = pa.lib()
+    w = pa.QMat(2, 8, 64, weights(2, 8, 64, 1))
+    x = torch.zeros(65, device="cuda")
+    y = torch.zeros(16, device="cuda")
+    assert lib.pai_qgemm_f32_async(w.handle, 0, x.data_ptr(), y.data_ptr(), 1, None) == -1
+    assert lib.pai_qgemm_f32_async(w.handle, 1, x.data_ptr() + 4, y.data_ptr(), 1, None) == -1
+    assert lib.pai_qgemm_f32_async(w.handle, 1, None, y.data_ptr(), 1, None) == -1
+    t, nn, kk = C.c_uint32(), C.c_uint64(), C.c_uint64()
+    assert lib.pai_qmat_shape(w.handle, C.byref(t), C.byref(nn), C.byref(kk)) == 0
+    assert (t.value, nn.value, kk.value) == (2, 8, 64)
+    assert w.nbytes == 8 * 36
