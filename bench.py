@@ -70,14 +70,16 @@ def quantized_layer(pa, qtype: int, config: int) -> list:
     return out
 
 
-def run_layers(pa, torch, layers, m: int, steps: int, warmup: int, per_launch_events: bool):
-    """Time `steps` passes over the seven projections, rotating layers."""
-    stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
+def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, per_launch_events: bool):
+    """Time `steps` passes over the seven projections, rotating layers.
+    Every launch goes to one HIP stream; the per-launch events are recorded
+    on that stream."""
+    stream = hm.Stream()
+    sh = stream.handle
     kmax = max(k for _, _, k in PROJ)
-    x = torch.from_numpy(pa.normal_f32(0xC0DE0000 ^ 0x5A5A, m * kmax).reshape(m, kmax)).cuda()
-    ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _, n, _ in PROJ]
-    xp, yp = x.data_ptr(), [y.data_ptr() for y in ys]
+    x = hm.DeviceBuffer.from_array(pa.normal_f32(0xC0DE0000 ^ 0x5A5A, m * kmax))
+    ys = [hm.DeviceBuffer(m * n * 4) for _, n, _ in PROJ]
+    xp, yp = x.ptr, [y.ptr for y in ys]
 
     def step(s, evs=None):
         layer = layers[s % len(layers)]
@@ -92,29 +94,34 @@ def run_layers(pa, torch, layers, m: int, steps: int, warmup: int, per_launch_ev
         step(s)
     evs = None
     if per_launch_events:
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(PROJ))]
-               for _ in range(steps)]
-    torch.cuda.synchronize()
+        evs = [[hm.Event() for _ in range(2 * len(PROJ))] for _ in range(steps)]
+    stream.synchronize()
     t0 = time.perf_counter()
     for s in range(steps):
         step(s, evs[s] if evs else None)
-    torch.cuda.synchronize()
+    stream.synchronize()
     wall = time.perf_counter() - t0
     per_proj_ms = None
     if evs:
         per_proj_ms = np.zeros(len(PROJ))
         for e in evs:
             for j in range(len(PROJ)):
-                per_proj_ms[j] += e[2 * j].elapsed_time(e[2 * j + 1])
+                per_proj_ms[j] += e[2 * j].elapsed_ms(e[2 * j + 1])
         per_proj_ms /= steps
+        for e in evs:
+            for ev in e:
+                ev.destroy()
+    for b in [x, *ys]:
+        b.free()
+    stream.destroy()
     return wall, per_proj_ms
 
 
-def gemv_config(pa, torch, qtype: int, config: int, m: int, nlayers: int, steps: int,
+def gemv_config(pa, hm, qtype: int, config: int, m: int, nlayers: int, steps: int,
                 warmup: int, per_launch_events: bool = True) -> dict:
     blocks = quantized_layer(pa, qtype, config)
     layers = [Layer(pa, qtype, blocks) for _ in range(nlayers)]
-    wall, per_ms = run_layers(pa, torch, layers, m, steps, warmup, per_launch_events)
+    wall, per_ms = run_layers(pa, hm, layers, m, steps, warmup, per_launch_events)
     bytes_step = sum(call_bytes(pa, qtype, n, k, m) for _, n, k in PROJ)
     res = {"qtype": qtype, "m": m, "layers": nlayers, "steps": steps,
            "weight_set_MB": round(nlayers * sum(l.nbytes for l in layers[0].w) / 1e6, 1),
@@ -133,23 +140,32 @@ def gemv_config(pa, torch, qtype: int, config: int, m: int, nlayers: int, steps:
     return res
 
 
-def q8_config1(pa, torch, steps: int) -> dict:
+def timed_calls(hm, call, reps: int, warm: int) -> float:
+    """Mean microseconds per call of `call(stream_handle, i)` between two
+    events on one stream."""
+    st = hm.Stream()
+    for i in range(warm):
+        call(st.handle, i)
+    a, b = hm.Event(), hm.Event()
+    a.record(st)
+    for i in range(reps):
+        call(st.handle, i)
+    b.record(st)
+    b.synchronize()
+    us = a.elapsed_ms(b) / reps * 1e3
+    a.destroy(); b.destroy(); st.destroy()
+    return us
+
+
+def q8_config1(pa, hm, steps: int) -> dict:
     n = k = 4096
     w = pa.normal_f32(seed_w(1, 0), n * k, 0.0, 0.02).reshape(n, k)
     blocks = pa.quantize(pa.Q8_0, w)
     copies = [pa.QMat(pa.Q8_0, n, k, blocks) for _ in range(32)]  # 570 MB
-    x = torch.from_numpy(pa.normal_f32(seed_w(1, 0) ^ 0x5A5A, k)).cuda()
-    y = torch.empty(n, device="cuda")
-    sh = torch.cuda.current_stream().cuda_stream
-    for i in range(64):
-        copies[i % 32].gemm_async(x.data_ptr(), y.data_ptr(), 1, 0, sh)
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(steps):
-        copies[i % 32].gemm_async(x.data_ptr(), y.data_ptr(), 1, 0, sh)
-    e.record()
-    torch.cuda.synchronize()
-    us = s.elapsed_time(e) / steps * 1e3
+    x = hm.DeviceBuffer.from_array(pa.normal_f32(seed_w(1, 0) ^ 0x5A5A, k))
+    y = hm.DeviceBuffer(n * 4)
+    us = timed_calls(hm, lambda sh, i: copies[i % 32].gemm_async(x.ptr, y.ptr, 1, 0, sh),
+                     steps, 64)
     b = call_bytes(pa, pa.Q8_0, n, k)
     for c in copies:
         c.free()
@@ -157,29 +173,20 @@ def q8_config1(pa, torch, steps: int) -> dict:
             "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
-def prefill(pa, torch, reps: int) -> dict:
+def prefill(pa, hm, reps: int) -> dict:
     out = {}
     m = 512
     for name, qtype, (n, k), cfg in (("gate_q4_k", pa.Q4_K, (14336, 4096), 4),
                                      ("down_q6_k", pa.Q6_K, (4096, 14336), 4)):
         w = pa.normal_f32(seed_w(cfg, 0 if qtype == pa.Q4_K else 6), n * k, 0.0, 0.02)
         qm = pa.QMat(qtype, n, k, pa.quantize(qtype, w.reshape(n, k)))
-        x = torch.from_numpy(pa.normal_f32(seed_w(cfg, 9), m * k).reshape(m, k)).cuda()
-        y = torch.empty((m, n), device="cuda")
-        sh = torch.cuda.current_stream().cuda_stream
-        for _ in range(3):
-            qm.gemm_async(x.data_ptr(), y.data_ptr(), m, 0, sh)
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(reps):
-            qm.gemm_async(x.data_ptr(), y.data_ptr(), m, 0, sh)
-        e.record()
-        torch.cuda.synchronize()
-        us = s.elapsed_time(e) / reps * 1e3
+        x = hm.DeviceBuffer.from_array(pa.normal_f32(seed_w(cfg, 9), m * k))
+        y = hm.DeviceBuffer(m * n * 4)
+        us = timed_calls(hm, lambda sh, i: qm.gemm_async(x.ptr, y.ptr, m, 0, sh), reps, 3)
         tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
         out[name] = {"us": round(us, 1), "TFLOPs": round(tflops, 1),
                      "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 3)}
-        qm.free()
+        qm.free(); x.free(); y.free()
     return out
 
 
@@ -251,12 +258,12 @@ def main() -> int:
               f"(the path has no multi-GPU sharding in this build)", file=sys.stderr)
         return 2
 
-    import torch
     import prosperoai_amd as pa
+    from prosperoai_amd import hipmem as hm
     pa.init()
-    log(f"device {torch.cuda.get_device_name(0)}; Q4_0 M=1 x {args.layers} layers")
+    log(f"Q4_0 M=1 x {args.layers} layers")
 
-    head = gemv_config(pa, torch, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup)
+    head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup)
     log(f"Q4_0 M=1: {head['GBps']:.1f} GB/s wall, {head.get('kernel_GBps', 0):.1f} GB/s kernels")
     roof = {"bound": "hbm", "achieved": round(head["kernel_GBps"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(head["kernel_GBps"] / HBM_PEAK_GBS, 4),
@@ -271,14 +278,14 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         try:
-            extra["q4_k_m1"] = gemv_config(pa, torch, pa.Q4_K, 3, 1, args.layers, 300, 20)
+            extra["q4_k_m1"] = gemv_config(pa, hm, pa.Q4_K, 3, 1, args.layers, 300, 20)
             log(f"Q4_K M=1: {extra['q4_k_m1']['kernel_GBps']:.1f} GB/s kernels")
             for m in (8, 32):
-                extra[f"q4_k_m{m}"] = gemv_config(pa, torch, pa.Q4_K, 3, m, args.layers, 100, 5,
+                extra[f"q4_k_m{m}"] = gemv_config(pa, hm, pa.Q4_K, 3, m, args.layers, 100, 5,
                                                   per_launch_events=False)
                 log(f"Q4_K M={m}: {extra[f'q4_k_m{m}']['GBps']:.1f} GB/s")
-            extra["q8_0_4096x4096_m1"] = q8_config1(pa, torch, 300)
-            extra["prefill_m512"] = prefill(pa, torch, 20)
+            extra["q8_0_4096x4096_m1"] = q8_config1(pa, hm, 300)
+            extra["prefill_m512"] = prefill(pa, hm, 20)
             log(f"prefill: {extra['prefill_m512']}")
         except Exception as e:  # extras never hide the headline
             extra["error"] = repr(e)

@@ -211,41 +211,42 @@ def test_prefill_shape_gate_q4k_m512():
 
 # ------------------------------------------------------------------ device pointers
 def test_device_pointer_path_matches_host_path():
-    import torch
+    from prosperoai_amd.hipmem import DeviceBuffer, Stream
     qtype, n, k = 12, 512, 2048
     say("[gpu] device-pointer path")
     blocks = weights(qtype, n, k, 4)
     w = pa.QMat(qtype, n, k, blocks)
+    stream = Stream()
     for m in (1, 3, 40):
         x = pa.normal_f32(m, m * k).reshape(m, k)
-        xd = torch.from_numpy(x).cuda()
-        yd = torch.empty((m, n), dtype=torch.float32, device="cuda")
-        stream = torch.cuda.current_stream().cuda_stream
-        w.gemm_async(xd.data_ptr(), yd.data_ptr(), m, 0, stream)
-        torch.cuda.synchronize()
-        assert np.array_equal(yd.cpu().numpy(), w.gemm(x))
+        xd = DeviceBuffer.from_array(x)
+        yd = DeviceBuffer(m * n * 4)
+        w.gemm_async(xd.ptr, yd.ptr, m, 0, stream.handle)
+        stream.synchronize()
+        assert np.array_equal(yd.download((m, n)), w.gemm(x))
+    stream.destroy()
 
 
 def test_upload_from_device_blocks():
-    import torch
+    from prosperoai_amd.hipmem import DeviceBuffer
     qtype, n, k = 14, 40, 512
     say("[gpu] upload from device")
     blocks = weights(qtype, n, k, 8)
-    dev = torch.from_numpy(blocks.reshape(-1)).cuda()
-    w2 = pa.QMat(qtype, n, k, None, device_ptr=dev.data_ptr())
+    dev = DeviceBuffer.from_array(blocks.reshape(-1))
+    w2 = pa.QMat(qtype, n, k, None, device_ptr=dev.ptr)
     assert np.array_equal(w2.dequant(), pa.QMat(qtype, n, k, blocks).dequant())
 
 
 def test_gpu_argument_errors():
-    import torch
+    from prosperoai_amd.hipmem import DeviceBuffer
     say("[gpu] argument errors")
     lib = pa.lib()
     w = pa.QMat(2, 8, 64, weights(2, 8, 64, 1))
-    x = torch.zeros(65, device="cuda")
-    y = torch.zeros(16, device="cuda")
-    assert lib.pai_qgemm_f32_async(w.handle, 0, x.data_ptr(), y.data_ptr(), 1, None) == -1
-    assert lib.pai_qgemm_f32_async(w.handle, 1, x.data_ptr() + 4, y.data_ptr(), 1, None) == -1
-    assert lib.pai_qgemm_f32_async(w.handle, 1, None, y.data_ptr(), 1, None) == -1
+    x = DeviceBuffer(65 * 4)
+    y = DeviceBuffer(16 * 4)
+    assert lib.pai_qgemm_f32_async(w.handle, 0, x.ptr, y.ptr, 1, None) == -1
+    assert lib.pai_qgemm_f32_async(w.handle, 1, x.ptr + 4, y.ptr, 1, None) == -1
+    assert lib.pai_qgemm_f32_async(w.handle, 1, None, y.ptr, 1, None) == -1
     t, nn, kk = C.c_uint32(), C.c_uint64(), C.c_uint64()
     assert lib.pai_qmat_shape(w.handle, C.byref(t), C.byref(nn), C.byref(kk)) == 0
     assert (t.value, nn.value, kk.value) == (2, 8, 64)
