@@ -1,24 +1,29 @@
 /*
  * Device-side block formats for gfx950.
  *
- * Every kernel works on "chunks": 32 consecutive codes of one row as seen
- * by one lane (chunk c covers a fixed set of 32 columns; K/32 chunks per
- * row). A chunk is fetched with one 16-byte code load (two for Q8_0) plus
- * its block's scales, decoded in registers, and either dequantized exactly
- * (the reference's f32 formula and operation order) or reduced against
- * activations.
+ * Every kernel works on "chunks": the 32 consecutive columns 32c..32c+31 of
+ * one row (K/32 chunks per row). The upload re-layout (qlayout.hip) stores
+ * the codes of a chunk contiguously, so one lane fetches a chunk with one
+ * 16-byte load of 4-bit codes (two for Q8_0's int8 codes; Q6_K adds an
+ * 8-byte load of its 2-bit high parts) plus the scales of its block.
+ *
+ * 4-bit code byte order inside a chunk (Q4_0, Q4_K, Q6_K low bits):
+ *   byte i (0..15): low nibble = column i, high nibble = column 16 + i.
+ * This is the native Q4_0 order; Q4_K and Q6_K are regrouped into it.
  *
  * Per format, F provides:
  *   Raw                 the bytes of one chunk, as loaded
  *   load(v, row, c)     fetch chunk c of a row from the device planes
- *   elem(c, i)          column of slot i (0..31) of chunk c
- *   kRun                slots come in runs of kRun consecutive columns
- *   kNG                 slot groups sharing one scale (32/kNG slots each)
+ *   kNG                 slot groups sharing one scale: group g covers
+ *                       columns 16g..16g+15 (kNG = 2) or all 32 (kNG = 1)
+ *   kHiScale            columns 16..31 carry codes times 1/kHiScale
  *   decode(w, c, q, a, b)
- *                       q[i] = code of slot i as f32 (possibly scaled by a
- *                       power of two), and for group g the chunk's dot
- *                       product with x is  sum_g a[g]*sum(q*x) - b[g]*sum(x)
- *   dequant(w, c, o)    o[i] = the reference's f32 value of slot i, bit-exact
+ *                       q[i] = code of column i as f32 (times 1/kHiScale for
+ *                       i >= 16), and the chunk's dot product with x is
+ *                         sum_g a[g] * sum_{i in g} q[i] x'[i]  -  b[g] * sum_{i in g} x[i]
+ *                       with x'[i] = x[i] for i < 16, kHiScale * x[i] above
+ *   dequant(w, c, o)    o[i] = the reference's f32 value of column i,
+ *                       bit-exact (same operations, same order)
  */
 #ifndef PAI_QDEV_H
 #define PAI_QDEV_H
@@ -44,11 +49,43 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
 __device__ __forceinline__ uint2 ld8(const uint8_t *p) {
   return *reinterpret_cast<const uint2 *>(p);
 }
+__device__ __forceinline__ uint32_t ld2(const uint8_t *p) {
+  return *reinterpret_cast<const uint16_t *>(p);
+}
+
+__device__ __forceinline__ uint32_t word4(const uint4 &q, int j) {
+  return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+}
+
+/* Hides the known bits of v from the optimizer. Without it, LLVM folds
+ * "mask then take byte b" into a bit-field extract followed by
+ * v_cvt_f32_ubyte0 (two instructions per code); with it, each code
+ * converts in one v_cvt_f32_ubyte{0,1,2,3}. */
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  __asm__("" : "+v"(v));
+  return v;
+}
+
+/* q[4j+b] = low nibble of byte b of word j (column 4j+b); q[16+4j+b] =
+ * 16 * high nibble (column 16+4j+b). */
+__device__ __forceinline__ void nibbles_f32(const uint4 &qw, float q[32]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = word4(qw, j);
+    const uint32_t lo = opaque(w & 0x0F0F0F0Fu), hi = opaque(w & 0xF0F0F0F0u);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      q[4 * j + b] = (float)byte_of(lo, b);
+      q[16 + 4 * j + b] = (float)byte_of(hi, b);
+    }
+  }
+}
 
 /* ---------------------------------------------------------------- Q8_0 */
 /* adapters/llama/gguf.c:750-761: value = (float)int8 * d. */
 struct Q8_0 {
-  static constexpr uint32_t kType = 8, kRun = 32, kNG = 1;
+  static constexpr uint32_t kType = 8, kNG = 1;
+  static constexpr float kHiScale = 1.0f;
   struct Raw {
     uint4 q0, q1;
     uint32_t d;
@@ -61,20 +98,20 @@ struct Q8_0 {
     w.d = v.d[(size_t)row * v.nb + c];
     return w;
   }
-  __device__ static uint32_t elem(uint32_t c, int i) { return 32u * c + (uint32_t)i; }
   __device__ static uint32_t word(const Raw &w, int i) {
-    const uint32_t ws[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-    return ws[i];
+    return i < 4 ? word4(w.q0, i) : word4(w.q1, i - 4);
   }
+  /* q = code + 128 (the bytes with their sign bit flipped, read as
+   * unsigned), so the offset is b = 128 * d. */
   __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint32_t x = word(w, j);
+      const uint32_t x = opaque(word(w, j) ^ 0x80808080u);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) q[4 * j + i] = (float)(int32_t)(int8_t)byte_of(x, i);
+      for (int i = 0; i < 4; ++i) q[4 * j + i] = (float)byte_of(x, i);
     }
     a[0] = h2f(w.d);
-    b[0] = 0.0f;
+    b[0] = 128.0f * a[0];
   }
   __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
     const float d = h2f(w.d);
@@ -89,9 +126,11 @@ struct Q8_0 {
 
 /* ---------------------------------------------------------------- Q4_0 */
 /* adapters/llama/gguf.c:680-694: byte j -> element j (low nibble) and
- * element j+16 (high nibble), value = (float)(nibble - 8) * d. */
+ * element j+16 (high nibble), value = (float)(nibble - 8) * d. The chunk is
+ * the native block's 16 code bytes, unchanged. */
 struct Q4_0 {
-  static constexpr uint32_t kType = 2, kRun = 32, kNG = 2;
+  static constexpr uint32_t kType = 2, kNG = 1;
+  static constexpr float kHiScale = 0.0625f;
   struct Raw {
     uint4 q;
     uint32_t d;
@@ -102,31 +141,20 @@ struct Q4_0 {
     w.d = v.d[(size_t)row * v.nb + c];
     return w;
   }
-  __device__ static uint32_t elem(uint32_t c, int i) { return 32u * c + (uint32_t)i; }
   __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
-    const uint32_t ws[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = ws[j] & 0x0F0F0F0Fu, hi = ws[j] & 0xF0F0F0F0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        q[4 * j + i] = (float)byte_of(lo, i);
-        q[16 + 4 * j + i] = (float)byte_of(hi, i); /* 16 * code */
-      }
-    }
+    nibbles_f32(w.q, q);
     const float d = h2f(w.d);
     a[0] = d;
-    a[1] = d * 0.0625f;
-    b[0] = b[1] = 8.0f * d;
+    b[0] = 8.0f * d;
   }
   __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
     const float d = h2f(w.d);
-    const uint32_t ws[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const uint32_t x = word4(w.q, j);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t by = byte_of(ws[j], i);
+        const uint32_t by = byte_of(x, i);
         o[4 * j + i] = (float)((int32_t)(by & 0x0Fu) - 8) * d;
         o[16 + 4 * j + i] = (float)((int32_t)(by >> 4) - 8) * d;
       }
@@ -149,12 +177,13 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
   }
 }
 
-/* adapters/llama/gguf.c:852-882. Chunk c = (super-block b = c/8,
- * pair p = (c%8)/2, half hh = c%2) holds code bytes q[32p+16hh .. +16):
- * low nibbles are columns 256b+64p+16hh+i (scale pair 2p), high nibbles
- * are those +32 (pair 2p+1). Value = (d*sc)*q - (dmin*m). */
+/* adapters/llama/gguf.c:852-882. Chunk c is sub-block j = c % 8 of
+ * super-block c / 8 (columns 32j..32j+31 of it), which the reference
+ * dequantizes as d1 * q - m1 with d1 = d * sc_j, m1 = dmin * m_j. Its 32
+ * nibbles are stored in the 4-bit chunk order. */
 struct Q4_K {
-  static constexpr uint32_t kType = 12, kRun = 16, kNG = 2;
+  static constexpr uint32_t kType = 12, kNG = 1;
+  static constexpr float kHiScale = 0.0625f;
   struct Raw {
     uint4 q;
     uint4 m; /* d | dmin<<16, scales[0..3], scales[4..7], scales[8..11] */
@@ -165,130 +194,96 @@ struct Q4_K {
     w.m = ld16(v.meta + ((size_t)row * v.nb + (c >> 3)) * 16u);
     return w;
   }
-  __device__ static uint32_t elem(uint32_t c, int i) {
-    const uint32_t r = c & 7u;
-    return 256u * (c >> 3) + 64u * (r >> 1) + 16u * (r & 1u) + (uint32_t)(i & 15) +
-           (i >= 16 ? 32u : 0u);
-  }
-  __device__ static void scales(const Raw &w, uint32_t c, float &d1, float &m1, float &d2,
-                                float &m2) {
-    const uint32_t p = (c & 7u) >> 1;
-    uint32_t s0, n0, s1, n1;
-    scale_min_k4(2u * p, w.m.y, w.m.z, w.m.w, s0, n0);
-    scale_min_k4(2u * p + 1u, w.m.y, w.m.z, w.m.w, s1, n1);
-    const float d = h2f(w.m.x), dmin = h2f(w.m.x >> 16);
-    d1 = d * (float)s0;
-    m1 = dmin * (float)n0;
-    d2 = d * (float)s1;
-    m2 = dmin * (float)n1;
+  __device__ static void scales(const Raw &w, uint32_t c, float &d1, float &m1) {
+    uint32_t s, mn;
+    scale_min_k4(c & 7u, w.m.y, w.m.z, w.m.w, s, mn);
+    d1 = h2f(w.m.x) * (float)s;
+    m1 = h2f(w.m.x >> 16) * (float)mn;
   }
   __device__ static void decode(const Raw &w, uint32_t c, float q[32], float a[kNG], float b[kNG]) {
-    const uint32_t ws[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = ws[j] & 0x0F0F0F0Fu, hi = ws[j] & 0xF0F0F0F0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        q[4 * j + i] = (float)byte_of(lo, i);
-        q[16 + 4 * j + i] = (float)byte_of(hi, i); /* 16 * code */
-      }
-    }
-    float d1, m1, d2, m2;
-    scales(w, c, d1, m1, d2, m2);
-    a[0] = d1;
-    b[0] = m1;
-    a[1] = d2 * 0.0625f;
-    b[1] = m2;
+    nibbles_f32(w.q, q);
+    scales(w, c, a[0], b[0]);
   }
   __device__ static void dequant(const Raw &w, uint32_t c, float o[32]) {
-    float d1, m1, d2, m2;
-    scales(w, c, d1, m1, d2, m2);
-    const uint32_t ws[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+    float d1, m1;
+    scales(w, c, d1, m1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const uint32_t x = word4(w.q, j);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t by = byte_of(ws[j], i);
+        const uint32_t by = byte_of(x, i);
         o[4 * j + i] = d1 * (float)(by & 0x0Fu) - m1;
-        o[16 + 4 * j + i] = d2 * (float)(by >> 4) - m2;
+        o[16 + 4 * j + i] = d1 * (float)(by >> 4) - m1;
       }
     }
   }
 };
 
 /* ---------------------------------------------------------------- Q6_K */
-/* adapters/llama/gguf.c:920-947. Chunk c = (super-block b = c/8,
- * half h = (c%8)/4, t = c%4) covers l = 8t..8t+7 of half h; slot 8g+i is
- * column 256b+128h+32g+8t+i with scale sc[8h + t/2 + 2g] and code
- *   g=0: ql[l] low | qh[l] bits 0-1      g=1: ql[l+32] low | bits 2-3
- *   g=2: ql[l] high | qh[l] bits 4-5     g=3: ql[l+32] high | bits 6-7
- * Value = d * sc * (code - 32), left to right. */
+/* adapters/llama/gguf.c:920-947. Chunk c = 4h + g of a super-block covers
+ * its columns 128h + 32g + l (l < 32), with scale sc[8h + 2g + l/16], i.e.
+ * sc[2(c%8)] for columns 0..15 of the chunk and sc[2(c%8)+1] for 16..31,
+ * and 6-bit code q = low4 | high2 << 4; value = d * sc * (q - 32), left to
+ * right. Storage: the low 4 bits in the 4-bit chunk order; the high 2 bits
+ * as two words e0 (columns 0..15) and e1 (16..31), column 16t + 4k + b at
+ * bits 2k..2k+1 of byte b of e_t. */
 struct Q6_K {
-  static constexpr uint32_t kType = 14, kRun = 8, kNG = 4;
+  static constexpr uint32_t kType = 14, kNG = 2;
+  static constexpr float kHiScale = 1.0f;
   struct Raw {
-    uint4 ql; /* ql[l] for the 8 l's, then ql[l+32] */
+    uint4 ql;
     uint2 qh;
-    uint2 sc; /* scales[8h .. 8h+7] */
+    uint32_t sc; /* int8 scales of columns 0..15 | 16..31 << 8 */
     uint32_t d;
   };
   __device__ static Raw load(const paik_qview_t &v, uint32_t row, uint32_t c) {
-    const uint32_t b = c >> 3, r = c & 7u;
+    const size_t blk = (size_t)row * v.nb + (c >> 3);
     Raw w;
     w.ql = ld16(v.q + (size_t)row * v.q_stride + 16u * c);
-    w.qh = ld8(v.aux + (size_t)row * (v.k >> 2) + 64u * b + 8u * r);
-    w.sc = ld8(v.meta + ((size_t)row * v.nb + b) * 16u + 8u * (r >> 2));
-    w.d = v.d[(size_t)row * v.nb + b];
+    w.qh = ld8(v.aux + (size_t)row * (v.k >> 2) + 8u * c);
+    w.sc = ld2(v.meta + blk * 16u + 2u * (c & 7u));
+    w.d = v.d[blk];
     return w;
   }
-  __device__ static uint32_t elem(uint32_t c, int i) {
-    const uint32_t r = c & 7u;
-    return 256u * (c >> 3) + 128u * (r >> 2) + 32u * (uint32_t)(i >> 3) + 8u * (r & 3u) +
-           (uint32_t)(i & 7);
+  /* 6-bit codes of word j: columns 4j+b (hi = 0) or 16+4j+b (hi = 1). */
+  __device__ static uint32_t codes(const Raw &w, int j, int hi) {
+    const uint32_t x = word4(w.ql, j);
+    const uint32_t lo4 = hi ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
+    const uint32_t e = hi ? w.qh.y : w.qh.x;
+    return opaque(lo4 | (((e >> (2 * j)) & 0x03030303u) << 4));
   }
-  /* codes of group g for the four l's of word j (0: l=8t..8t+3, 1: +4..+7) */
-  __device__ static uint32_t codes(const Raw &w, int g, int j) {
-    const uint32_t a = j ? w.ql.y : w.ql.x;
-    const uint32_t cc = j ? w.ql.w : w.ql.z;
-    const uint32_t e = j ? w.qh.y : w.qh.x;
-    switch (g) {
-    case 0: return (a & 0x0F0F0F0Fu) | ((e & 0x03030303u) << 4);
-    case 1: return (cc & 0x0F0F0F0Fu) | ((e & 0x0C0C0C0Cu) << 2);
-    case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u);
-    default: return ((cc >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u);
-    }
+  __device__ static float scale(const Raw &w, int g) {
+    return (float)(int32_t)(int8_t)byte_of(w.sc, g);
   }
-  __device__ static int32_t scale(const Raw &w, uint32_t c, int g) {
-    const uint32_t t2 = (c & 3u) >> 1; /* t/2 */
-    const uint32_t word = g < 2 ? w.sc.x : w.sc.y;
-    return (int32_t)(int8_t)byte_of(word, (int)(t2 + 2u * (uint32_t)(g & 1)));
-  }
-  __device__ static void decode(const Raw &w, uint32_t c, float q[32], float a[kNG], float b[kNG]) {
-    const float d = h2f(w.d);
+  __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 2; ++g) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t cw = codes(w, g, j);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t cw = codes(w, j, g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[8 * g + 4 * j + i] = (float)byte_of(cw, i);
+        for (int i = 0; i < 4; ++i) q[16 * g + 4 * j + i] = (float)byte_of(cw, i);
       }
-      const float ds = d * (float)scale(w, c, g);
-      a[g] = ds;
-      b[g] = 32.0f * ds;
     }
-  }
-  __device__ static void dequant(const Raw &w, uint32_t c, float o[32]) {
     const float d = h2f(w.d);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float s = (float)scale(w, c, g);
+    for (int g = 0; g < 2; ++g) {
+      a[g] = d * scale(w, g);
+      b[g] = 32.0f * a[g];
+    }
+  }
+  __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
+    const float d = h2f(w.d);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t cw = codes(w, g, j);
+    for (int g = 0; g < 2; ++g) {
+      const float s = scale(w, g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          o[8 * g + 4 * j + i] = d * s * (float)((int32_t)byte_of(cw, i) - 32);
-        }
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t cw = codes(w, j, g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[16 * g + 4 * j + i] = d * s * (float)((int32_t)byte_of(cw, i) - 32);
       }
     }
   }

@@ -89,7 +89,7 @@ __global__ void __launch_bounds__(256) k_gemm(paik_qview_t v, const float *__res
       }
 #pragma unroll
       for (int i = 0; i < 32; i += 8) {
-        const uint32_t e = (c < nchunks ? F::elem(c, i) : 32u * c + (uint32_t)i) - k0;
+        const uint32_t e = 32u * c + (uint32_t)i - k0;
         uint4 p;
         p.x = pack2(to16<BF>(o[i]), to16<BF>(o[i + 1]));
         p.y = pack2(to16<BF>(o[i + 2]), to16<BF>(o[i + 3]));
