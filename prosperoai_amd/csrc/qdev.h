@@ -4,26 +4,35 @@
  * Every kernel works on "chunks": the 32 consecutive columns 32c..32c+31 of
  * one row (K/32 chunks per row). The upload re-layout (qlayout.hip) stores
  * the codes of a chunk contiguously, so one lane fetches a chunk with one
- * 16-byte load of 4-bit codes (two for Q8_0's int8 codes; Q6_K adds an
- * 8-byte load of its 2-bit high parts) plus the scales of its block.
+ * 16-byte load of 4-bit codes (two for Q8_0; Q6_K adds an 8-byte load of
+ * its 2-bit high parts) plus the scales of its block.
  *
- * 4-bit code byte order inside a chunk (Q4_0, Q4_K, Q6_K low bits):
- *   byte i (0..15): low nibble = column i, high nibble = column 16 + i.
- * This is the native Q4_0 order; Q4_K and Q6_K are regrouped into it.
+ * Nibble words. 16 bytes of 4-bit fields hold a chunk as four 32-bit words;
+ * word j carries columns 8j..8j+7: byte m (0..3) of the word holds column
+ * 8j+m in its low nibble and column 8j+m+4 in its high nibble. (The digit
+ * planes of the activations are built by byte gathers in this order.)
+ * Fields are signed 4-bit integers wherever the format allows, so
+ * v_dot8_i32_i4 can consume them as stored:
+ *   Q4_0, Q4_K  s = n - 8 (the code n with its top bit flipped)
+ *   Q8_0        low word group:  s = l - 8 for the low nibble l of the code,
+ *               high word group: h, the code's (signed) high nibble, so
+ *               code = 16 h + s + 8
+ *   Q6_K        low 4 bits as s = l - 8; the high 2 bits h2 (0..3) in a
+ *               separate 8-byte group: word e_t (t = 0, 1) keeps column
+ *               16t + i (i < 8) at bits o..o+1 and column 16t + 8 + i at
+ *               bits o+2..o+3, o being column i's nibble offset in a nibble
+ *               word, so e_t & 0x33333333 and (e_t >> 2) & 0x33333333 are
+ *               nibble words; q = 16 h2 + s + 8
  *
  * Per format, F provides:
  *   Raw                 the bytes of one chunk, as loaded
  *   load(v, row, c)     fetch chunk c of a row from the device planes
- *   kNG                 slot groups sharing one scale: group g covers
- *                       columns 16g..16g+15 (kNG = 2) or all 32 (kNG = 1)
- *   kHiScale            columns 16..31 carry codes times 1/kHiScale
- *   decode(w, c, q, a, b)
- *                       q[i] = code of column i as f32 (times 1/kHiScale for
- *                       i >= 16), and the chunk's dot product with x is
- *                         sum_g a[g] * sum_{i in g} q[i] x'[i]  -  b[g] * sum_{i in g} x[i]
- *                       with x'[i] = x[i] for i < 16, kHiScale * x[i] above
+ *   bload(r, row, cb, l) the same for chunk cb + l through plane buffer
+ *                       resources (row and cb wave-uniform, l the lane)
  *   dequant(w, c, o)    o[i] = the reference's f32 value of column i,
  *                       bit-exact (same operations, same order)
+ *   dot(w, c, x)        the chunk's dot product with an activation chunk
+ *                       given as digit planes (XChunk below)
  */
 #ifndef PAI_QDEV_H
 #define PAI_QDEV_H
@@ -35,11 +44,14 @@
 
 namespace paik {
 
-__device__ __forceinline__ float h2f(uint32_t bits) {
+__device__ __forceinline__ float h2f(uint16_t bits) {
   // v_cvt_f32_f16 is exact for zeros, subnormals, normals and infinities;
   // a NaN stays a NaN (its payload is quieted, unlike a bit copy).
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+  return (float)__builtin_bit_cast(_Float16, bits);
 }
+/* f16 in the low / high half of a 32-bit word */
+__device__ __forceinline__ float h2f_lo(uint32_t w) { return h2f((uint16_t)w); }
+__device__ __forceinline__ float h2f_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 
@@ -49,7 +61,7 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
 __device__ __forceinline__ uint2 ld8(const uint8_t *p) {
   return *reinterpret_cast<const uint2 *>(p);
 }
-__device__ __forceinline__ uint32_t ld2(const uint8_t *p) {
+__device__ __forceinline__ uint16_t ld2(const uint8_t *p) {
   return *reinterpret_cast<const uint16_t *>(p);
 }
 
@@ -57,83 +69,176 @@ __device__ __forceinline__ uint32_t word4(const uint4 &q, int j) {
   return j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
 }
 
-/* Hides the known bits of v from the optimizer. Without it, LLVM folds
- * "mask then take byte b" into a bit-field extract followed by
- * v_cvt_f32_ubyte0 (two instructions per code); with it, each code
- * converts in one v_cvt_f32_ubyte{0,1,2,3}. */
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-  __asm__("" : "+v"(v));
-  return v;
+/* ------------------------------------------------------------------------
+ * Buffer-resource view of a packed matrix for the streaming kernels: one
+ * 128-bit resource per plane (base, byte size; reads past the size return
+ * zero), so a load is "plane resource + wave-uniform byte offset (SGPR) +
+ * lane offset (VGPR)" with no per-lane 64-bit address arithmetic.
+ * ---------------------------------------------------------------------- */
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct QRes {
+  __amdgpu_buffer_rsrc_t q, aux, meta, d;
+  uint32_t q_stride, nb, k4;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void *p, uint32_t bytes) {
+  /* 0x00020000: the gfx9 data-format word of a raw byte buffer */
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                           0x00020000);
 }
 
-/* q[4j+b] = low nibble of byte b of word j (column 4j+b); q[16+4j+b] =
- * 16 * high nibble (column 16+4j+b). */
-__device__ __forceinline__ void nibbles_f32(const uint4 &qw, float q[32]) {
+__device__ __forceinline__ QRes make_qres(const paik_qview_t &v) {
+  QRes r;
+  r.q = plane_rsrc(v.q, v.n * v.q_stride);
+  r.aux = plane_rsrc(v.aux, v.n * (v.k >> 2));
+  r.meta = plane_rsrc(v.meta, v.n * v.nb * 16u);
+  r.d = plane_rsrc(v.d, v.n * v.nb * 2u);
+  r.q_stride = v.q_stride;
+  r.nb = v.nb;
+  r.k4 = v.k >> 2;
+  return r;
+}
+
+__device__ __forceinline__ uint4 bl16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+__device__ __forceinline__ uint2 bl8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+  return make_uint2(x.x, x.y);
+}
+/* kept 16-bit: a zero-extension would be an early use of the load */
+__device__ __forceinline__ uint16_t bl2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
+/* Bit offset of column i (0..7) in a nibble word. */
+__host__ __device__ constexpr int nib_off(int i) { return 8 * (i & 3) + 4 * (i >> 2); }
+/* Signed 4-bit field of column i of a nibble word. */
+__device__ __forceinline__ int32_t snib(uint32_t w, int i) {
+  return (int32_t)(w << (28 - nib_off(i))) >> 28;
+}
+/* Unsigned 4-bit field of column i. */
+__device__ __forceinline__ uint32_t unib(uint32_t w, int i) { return (w >> nib_off(i)) & 0xFu; }
+
+/* ------------------------------------------------------------------------
+ * Activation digit planes.
+ *
+ * An activation chunk x[0..31] is represented exactly enough for an f32
+ * result by 24-bit fixed point relative to the chunk's largest magnitude:
+ * with 2^(E-1) <= max|x| < 2^E, xq[k] = rint(x[k] * 2^(22-E)), |xq| <= 2^22,
+ * and x[k] ~= xq[k] * xs with xs = 2^(E-22) (error <= 2^-23 max|x|). xq is
+ * written in six signed base-16 digits, xq = sum_i 16^i D_i with D_i in
+ * [-8, 7] (the nibbles of (xq + 0x888888) with their top bit flipped), and
+ * plane X[i] holds digit i of the 32 columns as four nibble words. Then for
+ * signed 4-bit codes s, sum_k s[k] xq[k] = sum_i 16^i sum_j dot8(s_j, X[i][j]).
+ * sx0 / sx1 are the sums of xq * xs over columns 0..15 / 16..31.
+ * A chunk holding an infinity or NaN gets xs = NaN, so every output that
+ * touches it is NaN.
+ * ---------------------------------------------------------------------- */
+struct XChunk {
+  uint32_t X[6][4];
+  float xs, sx0, sx1;
+};
+
+__device__ __forceinline__ int32_t dot8(uint32_t a, uint32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot8((int)a, (int)b, c, false);
+}
+/* dot8 into a fresh accumulator: the three-operand form with an inline
+ * zero (the compiler otherwise zeroes a register for v_dot8c first). */
+__device__ __forceinline__ int32_t dot8z(uint32_t a, uint32_t b) {
+  int32_t r;
+  __asm__("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+/* sum_i 16^i A[i] for i < NA (6 or 7), as f32. Each A[i] is at most 2^12
+ * in magnitude, so the integer steps cannot overflow. */
+template <int NA>
+__device__ __forceinline__ float combine(const int32_t A[NA]) {
+  const int32_t lo = A[0] + (A[1] << 4) + (A[2] << 8) + (A[3] << 12);
+  int32_t hi = A[4] + (A[5] << 4);
+  if constexpr (NA > 6) hi += A[6] << 8;
+  return fmaf((float)hi, 65536.0f, (float)lo);
+}
+
+/* A[i] += dot8(s_j, X[i][j]) for the words j in [J0, J1); with HI the words
+ * are high digits worth 16x and land in A[i + 1]. */
+template <bool HI, int J0, int J1>
+__device__ __forceinline__ void dots(const uint32_t *s, const XChunk &x, int32_t *A) {
+  constexpr int o = HI ? 1 : 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t w = word4(qw, j);
-    const uint32_t lo = opaque(w & 0x0F0F0F0Fu), hi = opaque(w & 0xF0F0F0F0u);
+  for (int j = J0; j < J1; ++j)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      q[4 * j + b] = (float)byte_of(lo, b);
-      q[16 + 4 * j + b] = (float)byte_of(hi, b);
-    }
-  }
+    for (int i = 0; i < 6; ++i) A[i + o] = dot8(s[j], x.X[i][j], A[i + o]);
+}
+/* Same, starting the six chains A[0..5] from zero (A[6] untouched). */
+template <int J0, int J1>
+__device__ __forceinline__ void dots0(const uint32_t *s, const XChunk &x, int32_t *A) {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) A[i] = dot8z(s[J0], x.X[i][J0]);
+#pragma unroll
+  for (int j = J0 + 1; j < J1; ++j)
+#pragma unroll
+    for (int i = 0; i < 6; ++i) A[i] = dot8(s[j], x.X[i][j], A[i]);
 }
 
 /* ---------------------------------------------------------------- Q8_0 */
 /* adapters/llama/gguf.c:750-761: value = (float)int8 * d. */
 struct Q8_0 {
-  static constexpr uint32_t kType = 8, kNG = 1;
-  static constexpr float kHiScale = 1.0f;
+  static constexpr uint32_t kType = 8;
   struct Raw {
-    uint4 q0, q1;
-    uint32_t d;
+    uint4 lo, hi; /* low-nibble words (l - 8), high-nibble words (h) */
+    uint16_t d;
   };
   __device__ static Raw load(const paik_qview_t &v, uint32_t row, uint32_t c) {
     const uint8_t *p = v.q + (size_t)row * v.q_stride + 32u * c;
     Raw w;
-    w.q0 = ld16(p);
-    w.q1 = ld16(p + 16);
+    w.lo = ld16(p);
+    w.hi = ld16(p + 16);
     w.d = v.d[(size_t)row * v.nb + c];
     return w;
   }
-  __device__ static uint32_t word(const Raw &w, int i) {
-    return i < 4 ? word4(w.q0, i) : word4(w.q1, i - 4);
+  /* chunk cb + lane of a row; row and cb wave-uniform */
+  __device__ static Raw bload(const QRes &r, uint32_t row, uint32_t cb, uint32_t lane) {
+    Raw w;
+    const uint32_t so = row * r.q_stride + 32u * cb;
+    w.lo = bl16(r.q, 32u * lane, so);
+    w.hi = bl16(r.q, 32u * lane + 16u, so);
+    w.d = bl2(r.d, 2u * lane, (row * r.nb + cb) * 2u);
+    return w;
   }
-  /* q = code + 128 (the bytes with their sign bit flipped, read as
-   * unsigned), so the offset is b = 128 * d. */
-  __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t x = opaque(word(w, j) ^ 0x80808080u);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) q[4 * j + i] = (float)byte_of(x, i);
-    }
-    a[0] = h2f(w.d);
-    b[0] = 128.0f * a[0];
+  __device__ static int32_t code(const Raw &w, int col) {
+    const int j = col >> 3, i = col & 7;
+    return 16 * snib(word4(w.hi, j), i) + snib(word4(w.lo, j), i) + 8;
   }
   __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
     const float d = h2f(w.d);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t x = word(w, j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[4 * j + i] = (float)(int32_t)(int8_t)byte_of(x, i) * d;
-    }
+    for (int k = 0; k < 32; ++k) o[k] = (float)code(w, k) * d;
+  }
+  /* code = 16 h + s + 8: sum code*x = [16 sum h xq + sum s xq] xs + 8 sum x */
+  __device__ static float dot(const Raw &w, uint32_t, const XChunk &x) {
+    const uint32_t s[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
+    const uint32_t h[4] = {w.hi.x, w.hi.y, w.hi.z, w.hi.w};
+    int32_t A[7];
+    dots0<0, 4>(s, x, A);
+    A[6] = 0;
+    dots<true, 0, 4>(h, x, A);
+    return h2f(w.d) * fmaf(combine<7>(A), x.xs, 8.0f * (x.sx0 + x.sx1));
   }
 };
 
 /* ---------------------------------------------------------------- Q4_0 */
-/* adapters/llama/gguf.c:680-694: byte j -> element j (low nibble) and
- * element j+16 (high nibble), value = (float)(nibble - 8) * d. The chunk is
- * the native block's 16 code bytes, unchanged. */
+/* adapters/llama/gguf.c:680-694: value = (float)(n - 8) * d, n the 4-bit
+ * code. Stored as s = n - 8. */
 struct Q4_0 {
-  static constexpr uint32_t kType = 2, kNG = 1;
-  static constexpr float kHiScale = 0.0625f;
+  static constexpr uint32_t kType = 2;
   struct Raw {
     uint4 q;
-    uint32_t d;
+    uint16_t d;
   };
   __device__ static Raw load(const paik_qview_t &v, uint32_t row, uint32_t c) {
     Raw w;
@@ -141,24 +246,22 @@ struct Q4_0 {
     w.d = v.d[(size_t)row * v.nb + c];
     return w;
   }
-  __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
-    nibbles_f32(w.q, q);
-    const float d = h2f(w.d);
-    a[0] = d;
-    b[0] = 8.0f * d;
+  __device__ static Raw bload(const QRes &r, uint32_t row, uint32_t cb, uint32_t lane) {
+    Raw w;
+    w.q = bl16(r.q, 16u * lane, row * r.q_stride + 16u * cb);
+    w.d = bl2(r.d, 2u * lane, (row * r.nb + cb) * 2u);
+    return w;
   }
   __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
     const float d = h2f(w.d);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t x = word4(w.q, j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t by = byte_of(x, i);
-        o[4 * j + i] = (float)((int32_t)(by & 0x0Fu) - 8) * d;
-        o[16 + 4 * j + i] = (float)((int32_t)(by >> 4) - 8) * d;
-      }
-    }
+    for (int k = 0; k < 32; ++k) o[k] = (float)snib(word4(w.q, k >> 3), k & 7) * d;
+  }
+  __device__ static float dot(const Raw &w, uint32_t, const XChunk &x) {
+    const uint32_t s[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+    int32_t A[6];
+    dots0<0, 4>(s, x, A);
+    return (h2f(w.d) * x.xs) * combine<6>(A);
   }
 };
 
@@ -179,11 +282,10 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
 
 /* adapters/llama/gguf.c:852-882. Chunk c is sub-block j = c % 8 of
  * super-block c / 8 (columns 32j..32j+31 of it), which the reference
- * dequantizes as d1 * q - m1 with d1 = d * sc_j, m1 = dmin * m_j. Its 32
- * nibbles are stored in the 4-bit chunk order. */
+ * dequantizes as d1 * n - m1 with d1 = d * sc_j, m1 = dmin * m_j. Codes are
+ * stored as s = n - 8. */
 struct Q4_K {
-  static constexpr uint32_t kType = 12, kNG = 1;
-  static constexpr float kHiScale = 0.0625f;
+  static constexpr uint32_t kType = 12;
   struct Raw {
     uint4 q;
     uint4 m; /* d | dmin<<16, scales[0..3], scales[4..7], scales[8..11] */
@@ -194,29 +296,34 @@ struct Q4_K {
     w.m = ld16(v.meta + ((size_t)row * v.nb + (c >> 3)) * 16u);
     return w;
   }
+  /* cb is a multiple of 8, so chunk cb + lane is in super-block
+   * cb/8 + lane/8 */
+  __device__ static Raw bload(const QRes &r, uint32_t row, uint32_t cb, uint32_t lane) {
+    Raw w;
+    w.q = bl16(r.q, 16u * lane, row * r.q_stride + 16u * cb);
+    w.m = bl16(r.meta, 16u * (lane >> 3), (row * r.nb + (cb >> 3)) * 16u);
+    return w;
+  }
   __device__ static void scales(const Raw &w, uint32_t c, float &d1, float &m1) {
     uint32_t s, mn;
     scale_min_k4(c & 7u, w.m.y, w.m.z, w.m.w, s, mn);
-    d1 = h2f(w.m.x) * (float)s;
-    m1 = h2f(w.m.x >> 16) * (float)mn;
-  }
-  __device__ static void decode(const Raw &w, uint32_t c, float q[32], float a[kNG], float b[kNG]) {
-    nibbles_f32(w.q, q);
-    scales(w, c, a[0], b[0]);
+    d1 = h2f_lo(w.m.x) * (float)s;
+    m1 = h2f_hi(w.m.x) * (float)mn;
   }
   __device__ static void dequant(const Raw &w, uint32_t c, float o[32]) {
     float d1, m1;
     scales(w, c, d1, m1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t x = word4(w.q, j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t by = byte_of(x, i);
-        o[4 * j + i] = d1 * (float)(by & 0x0Fu) - m1;
-        o[16 + 4 * j + i] = d1 * (float)(by >> 4) - m1;
-      }
-    }
+    for (int k = 0; k < 32; ++k) o[k] = d1 * (float)(unib(word4(w.q, k >> 3), k & 7) ^ 8u) - m1;
+  }
+  /* sum (d1 n - m1) x = d1 (sum s xq) xs + (8 d1 - m1) sum x */
+  __device__ static float dot(const Raw &w, uint32_t c, const XChunk &x) {
+    const uint32_t s[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+    int32_t A[6];
+    dots0<0, 4>(s, x, A);
+    float d1, m1;
+    scales(w, c, d1, m1);
+    return fmaf(d1 * x.xs, combine<6>(A), fmaf(8.0f, d1, -m1) * (x.sx0 + x.sx1));
   }
 };
 
@@ -225,17 +332,14 @@ struct Q4_K {
  * its columns 128h + 32g + l (l < 32), with scale sc[8h + 2g + l/16], i.e.
  * sc[2(c%8)] for columns 0..15 of the chunk and sc[2(c%8)+1] for 16..31,
  * and 6-bit code q = low4 | high2 << 4; value = d * sc * (q - 32), left to
- * right. Storage: the low 4 bits in the 4-bit chunk order; the high 2 bits
- * as two words e0 (columns 0..15) and e1 (16..31), column 16t + 4k + b at
- * bits 2k..2k+1 of byte b of e_t. */
+ * right. */
 struct Q6_K {
-  static constexpr uint32_t kType = 14, kNG = 2;
-  static constexpr float kHiScale = 1.0f;
+  static constexpr uint32_t kType = 14;
   struct Raw {
-    uint4 ql;
-    uint2 qh;
-    uint32_t sc; /* int8 scales of columns 0..15 | 16..31 << 8 */
-    uint32_t d;
+    uint4 ql;    /* s = low4 - 8, nibble words */
+    uint2 qh;    /* e0, e1 (see the top of this file) */
+    uint16_t sc; /* int8 scales of columns 0..15 | 16..31 << 8 */
+    uint16_t d;
   };
   __device__ static Raw load(const paik_qview_t &v, uint32_t row, uint32_t c) {
     const size_t blk = (size_t)row * v.nb + (c >> 3);
@@ -246,46 +350,53 @@ struct Q6_K {
     w.d = v.d[blk];
     return w;
   }
-  /* 6-bit codes of word j: columns 4j+b (hi = 0) or 16+4j+b (hi = 1). */
-  __device__ static uint32_t codes(const Raw &w, int j, int hi) {
-    const uint32_t x = word4(w.ql, j);
-    const uint32_t lo4 = hi ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu;
-    const uint32_t e = hi ? w.qh.y : w.qh.x;
-    return opaque(lo4 | (((e >> (2 * j)) & 0x03030303u) << 4));
+  __device__ static Raw bload(const QRes &r, uint32_t row, uint32_t cb, uint32_t lane) {
+    const uint32_t blk = row * r.nb + (cb >> 3);
+    Raw w;
+    w.ql = bl16(r.q, 16u * lane, row * r.q_stride + 16u * cb);
+    w.qh = bl8(r.aux, 8u * lane, row * r.k4 + 8u * cb);
+    w.sc = bl2(r.meta, 16u * (lane >> 3) + 2u * (lane & 7u), blk * 16u);
+    w.d = bl2(r.d, 2u * (lane >> 3), blk * 2u);
+    return w;
+  }
+  /* high-2-bit nibble words: word j covers columns 8j..8j+7 */
+  __device__ static void highs(const Raw &w, uint32_t h[4]) {
+    h[0] = w.qh.x & 0x33333333u;
+    h[1] = (w.qh.x >> 2) & 0x33333333u;
+    h[2] = w.qh.y & 0x33333333u;
+    h[3] = (w.qh.y >> 2) & 0x33333333u;
   }
   __device__ static float scale(const Raw &w, int g) {
-    return (float)(int32_t)(int8_t)byte_of(w.sc, g);
-  }
-  __device__ static void decode(const Raw &w, uint32_t, float q[32], float a[kNG], float b[kNG]) {
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t cw = codes(w, j, g);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) q[16 * g + 4 * j + i] = (float)byte_of(cw, i);
-      }
-    }
-    const float d = h2f(w.d);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      a[g] = d * scale(w, g);
-      b[g] = 32.0f * a[g];
-    }
+    return (float)(int32_t)(int8_t)(g ? (w.sc >> 8) : w.sc);
   }
   __device__ static void dequant(const Raw &w, uint32_t, float o[32]) {
     const float d = h2f(w.d);
+    uint32_t h[4];
+    highs(w, h);
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float s = scale(w, g);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t cw = codes(w, j, g);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          o[16 * g + 4 * j + i] = d * s * (float)((int32_t)byte_of(cw, i) - 32);
-      }
+    for (int k = 0; k < 32; ++k) {
+      const int j = k >> 3, i = k & 7;
+      const int32_t q = (int32_t)((unib(word4(w.ql, j), i) ^ 8u) | (unib(h[j], i) << 4));
+      o[k] = d * scale(w, k >> 4) * (float)(q - 32);
     }
+  }
+  /* q - 32 = 16 h2 + s - 24: per half g,
+   * sum (q - 32) x = [16 sum h2 xq + sum s xq] xs - 24 sum x */
+  __device__ static float dot(const Raw &w, uint32_t, const XChunk &x) {
+    const uint32_t s[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
+    uint32_t h[4];
+    highs(w, h);
+    int32_t A0[7], A1[7];
+    dots0<0, 2>(s, x, A0);
+    A0[6] = 0;
+    dots<true, 0, 2>(h, x, A0);
+    dots0<2, 4>(s, x, A1);
+    A1[6] = 0;
+    dots<true, 2, 4>(h, x, A1);
+    const float d = h2f(w.d);
+    const float t0 = fmaf(combine<7>(A0), x.xs, -24.0f * x.sx0);
+    const float t1 = fmaf(combine<7>(A1), x.xs, -24.0f * x.sx1);
+    return fmaf(d * scale(w, 0), t0, (d * scale(w, 1)) * t1);
   }
 };
 

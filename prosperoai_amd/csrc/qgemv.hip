@@ -1,44 +1,65 @@
 /*
- * Decode GEMV / small-batch GEMM over packed blocks (f32 arithmetic).
+ * Decode GEMV / small-batch GEMM over packed blocks with integer dot
+ * products (v_dot8_i32_i4).
  *
  * y[t][r] = sum_k x[t][k] * W[r][k] for up to MT tokens per launch.
  *
- * Work split (memory-bound path, HBM streaming of the code planes):
- *   - a "segment" is 64 chunks = 2048 columns: lane l of a wave owns chunk
- *     64s+l of every row, so the wave's 64 x 16-byte code loads of one row
- *     are one contiguous 1 KiB read (2 KiB for Q8_0);
- *   - a workgroup owns U rows and has one wave per segment (at most 8; a
- *     longer K loops over segments). Each wave issues the loads of all U
- *     rows of its segment before it decodes any, so U x 16 bytes per lane
- *     are in flight; the lane's 32 activations per token stay in registers
- *     for all U rows;
- *   - codes become f32 in registers (v_cvt_f32_ubyte*) and meet x in f32
- *     FMAs; per-group scales and code offsets are applied once per group
- *     from per-lane sums of x;
- *   - the U*MT per-lane partials of a wave are transposed through LDS
- *     (each lane then sums U*MT partials of one output) and finished with
- *     DPP row operations; the waves' sums are added in wave order. The
- *     summation order is fixed by the launch shape, so results do not
- *     depend on scheduling.
+ * Streaming design. The grid is about one 16-wave workgroup per CU; each
+ * wave owns a contiguous range of rows and walks it block by block, where
+ * a block is U rows x one 64-chunk step (lane l takes chunk 64s + l, so
+ * one row's loads of a block are one contiguous 1 KiB read). Each lane
+ * keeps 8 row-chunk loads in flight (a ring of 8/U blocks, refilled as
+ * each block is multiplied), so a 33 MB matrix on 4096 waves is requested
+ * in one pass and the dot products overlap the HBM stream.
+ *
+ * Per workgroup:
+ *   1. each wave issues the loads of its first 8/U blocks, then all threads
+ *      turn the activations of the launch's column slice into digit planes
+ *      in LDS (XChunk in qdev.h: six signed 4-bit digit planes of a 24-bit
+ *      fixed-point image of x with a per-chunk scale 2^(E-22)). Four
+ *      threads build one chunk, one nibble word of every plane each;
+ *   2. per block, a lane reads its chunk's planes from LDS once for the U
+ *      rows; a row-chunk costs 24 v_dot8 (48 for Q8_0 and Q6_K) and one
+ *      scale step;
+ *   3. after a row group's last step the wave sums each of its U*MT
+ *      per-lane partials across the 64 lanes in registers (DPP row steps,
+ *      then two cross-row steps). The summation order is fixed by the
+ *      launch shape, so results do not depend on scheduling.
+ *
+ * Rows longer than one slice (the chunks whose planes fit the 64 KiB LDS
+ * budget: 512 chunks = 16384 columns at MT = 1, U = 4) are covered by
+ * successive launches over column slices; all but the first add into y
+ * (each output is read and written by one lane, in launch order).
+ *
+ * The integer sums are exact; the roundings are the 24-bit image of x
+ * (<= 2^-23 of the chunk's largest |x|), the per-chunk scale steps and the
+ * f32 additions across chunks and lanes.
  */
 #include "qdev.h"
 
 namespace paik {
 
-constexpr int kMaxWaves = 8;
+constexpr int kWaves = 16;   /* waves per workgroup (one workgroup per CU) */
+constexpr int kInFlight = 8; /* row-chunk loads per lane kept in flight */
+constexpr size_t kLdsBudget = 65536; /* bytes of LDS per workgroup */
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E;
 
 /* Sum of v over aligned groups of L lanes (L a power of two <= 64); every
  * lane of a group receives the group's sum. */
 template <int L>
 __device__ __forceinline__ float group_sum(float v) {
-  if constexpr (L >= 2) v += dpp<0xB1>(v);   /* quad_perm [1,0,3,2]: lane ^ 1 */
-  if constexpr (L >= 4) v += dpp<0x4E>(v);   /* quad_perm [2,3,0,1]: lane ^ 2 */
+  if constexpr (L >= 2) v += dpp<kQuadXor1>(v);
+  if constexpr (L >= 4) v += dpp<kQuadXor2>(v);
   if constexpr (L >= 8) v += dpp<0x141>(v);  /* row_half_mirror: 8-lane halves */
   if constexpr (L >= 16) v += dpp<0x140>(v); /* row_mirror: 16-lane rows */
   if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
@@ -46,144 +67,298 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-template <class F, int U, int MT>
-__global__ void __launch_bounds__(512) k_gemv(paik_qview_t v, const float *__restrict__ x,
-                                              float *__restrict__ y, uint32_t ntok) {
-  constexpr int NG = (int)F::kNG, GS = 32 / NG;
-  constexpr int J = U * MT; /* outputs of the workgroup */
-  constexpr int L = 64 / J; /* lanes that finish one output */
-  static_assert(J >= 1 && J <= 64 && (J & (J - 1)) == 0, "U*MT must be a power of two <= 64");
-  __shared__ float tr[kMaxWaves][J * 64];
-  __shared__ float part[kMaxWaves][J];
+/* LDS image of one activation chunk. */
+struct XSlot {
+  uint4 X[6];
+};
+struct XScale {
+  float xs, sx0, sx1, pad;
+};
 
-  const int lane = (int)(threadIdx.x & 63u), wave = (int)(threadIdx.x >> 6);
-  const int nwaves = (int)(blockDim.x >> 6);
-  const uint32_t r0 = blockIdx.x * (uint32_t)U;
-  const uint32_t nchunks = v.k >> 5;
-  const uint32_t nseg = (nchunks + 63u) >> 6;
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
 
-  float p[U][MT];
+/* One quad-thread's share of a chunk: columns 8j..8j+7 (v[0..7]) of one
+ * token; writes word j of the six planes and, from threads 0 and 2 of the
+ * quad, the chunk's scale and half sums. */
+__device__ __forceinline__ void plane_words(const float v[8], uint32_t jw, XSlot *slot,
+                                            XScale *f) {
+  float m = 0.0f, sa = 0.0f;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) p[u][t] = 0.0f;
-
-  for (uint32_t s = (uint32_t)wave; s < nseg; s += (uint32_t)nwaves) {
-    const uint32_t c = 64u * s + (uint32_t)lane;
-    if (c < nchunks) {
-      typename F::Raw w[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) w[u] = F::load(v, min(r0 + (uint32_t)u, v.n - 1u), c);
-
-      float xs[MT][32], sx[MT][NG];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)t * v.k + 32u * c);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-          if ((uint32_t)t < ntok) f = src[i];
-          xs[t][4 * i] = f.x;
-          xs[t][4 * i + 1] = f.y;
-          xs[t][4 * i + 2] = f.z;
-          xs[t][4 * i + 3] = f.w;
-        }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          float a = 0.0f;
-#pragma unroll
-          for (int i = 0; i < GS; ++i) a += xs[t][g * GS + i];
-          sx[t][g] = a;
-        }
-        if constexpr (F::kHiScale != 1.0f) {
-#pragma unroll
-          for (int i = 16; i < 32; ++i) xs[t][i] *= F::kHiScale;
-        }
-      }
-
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float q[32], a[NG], b[NG];
-        F::decode(w[u], c, q, a, b);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          float acc = p[u][t];
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < GS; ++i) dot = fmaf(q[g * GS + i], xs[t][g * GS + i], dot);
-            acc = fmaf(a[g], dot, acc);
-            acc = fmaf(-b[g], sx[t][g], acc);
-          }
-          p[u][t] = acc;
-        }
-      }
-    }
+  for (int i = 0; i < 8; ++i) {
+    m = fmaxf(m, fabsf(v[i])); /* fmaxf drops NaNs ... */
+    sa += fabsf(v[i]);         /* ... which this sum keeps */
   }
-
-  /* Transpose: output j = u*MT + t, entry (j, lane) at tr[wave][j*64 + lane];
-   * lane l then sums entries (j = l / L, lanes (l % L)*J .. +J-1). */
-  float *T = tr[wave];
+  m = fmaxf(m, dpp<kQuadXor1>(m));
+  m = fmaxf(m, dpp<kQuadXor2>(m));
+  int bad = !(m <= 3.402823466e38f) || sa != sa;
+  bad |= dppi<kQuadXor1>(bad);
+  bad |= dppi<kQuadXor2>(bad);
+  const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : 0;
+  const int sh = bad ? 0 : 22 - e;
+  uint32_t u[8];
+  int sq = 0;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+  for (int i = 0; i < 8; ++i) {
+    const int q = bad ? 0 : (int)rintf(__builtin_amdgcn_ldexpf(v[i], sh));
+    sq += q;
+    u[i] = ((uint32_t)q + 0x888888u) ^ 0x888888u; /* bytes 0..2: digit pairs */
+  }
+  /* gather byte b of u0..u3 (lo) and u4..u7 (hi) */
+  const uint32_t a01 = perm(u[1], u[0], 0x05010400u), b01 = perm(u[1], u[0], 0x0C0C0602u);
+  const uint32_t a23 = perm(u[3], u[2], 0x05010400u), b23 = perm(u[3], u[2], 0x0C0C0602u);
+  const uint32_t a45 = perm(u[5], u[4], 0x05010400u), b45 = perm(u[5], u[4], 0x0C0C0602u);
+  const uint32_t a67 = perm(u[7], u[6], 0x05010400u), b67 = perm(u[7], u[6], 0x0C0C0602u);
+  const uint32_t g[3][2] = {{perm(a23, a01, 0x05040100u), perm(a67, a45, 0x05040100u)},
+                            {perm(a23, a01, 0x07060302u), perm(a67, a45, 0x07060302u)},
+                            {perm(b23, b01, 0x05040100u), perm(b67, b45, 0x05040100u)}};
+  uint32_t *dst = reinterpret_cast<uint32_t *>(slot) + jw;
 #pragma unroll
-    for (int t = 0; t < MT; ++t) T[(u * MT + t) * 64 + lane] = p[u][t];
-  __syncthreads();
-  const int j = lane / L, sub = lane % L;
-  float sum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < J; ++i) sum += T[j * 64 + sub * J + i];
-  sum = group_sum<L>(sum);
-  if (sub == 0) part[wave][j] = sum;
-  __syncthreads();
-  if ((int)threadIdx.x < J) {
-    const int jj = (int)threadIdx.x, u = jj / MT, t = jj % MT;
-    float acc = 0.0f;
-    for (int w = 0; w < nwaves; ++w) acc += part[w][jj];
-    if (r0 + (uint32_t)u < v.n && (uint32_t)t < ntok) y[(size_t)t * v.n + r0 + (uint32_t)u] = acc;
+  for (int b = 0; b < 3; ++b) {
+    /* byte m of a plane word = column m (low nibble) | column m+4 (high) */
+    dst[4 * (2 * b)] = (g[b][0] & 0x0F0F0F0Fu) | ((g[b][1] & 0x0F0F0F0Fu) << 4);
+    dst[4 * (2 * b + 1)] = ((g[b][0] >> 4) & 0x0F0F0F0Fu) | (g[b][1] & 0xF0F0F0F0u);
+  }
+  sq += dppi<kQuadXor1>(sq); /* words 0+1: columns 0..15; 2+3: 16..31 */
+  const float xs = bad ? __builtin_nanf("") : __builtin_amdgcn_ldexpf(1.0f, e - 22);
+  if (jw == 0u) {
+    f->xs = xs;
+    f->sx0 = (float)sq * xs;
+  } else if (jw == 2u) {
+    f->sx1 = (float)sq * xs;
   }
 }
 
-/* Rows per workgroup: the largest U (4, 8 or 16, with U*MT <= 16) whose
- * grid still puts about 8 waves on each of the 256 CUs. */
+/* Planes of chunks [cs, cs + nsc) for MT tokens, in two phases so that
+ * the activation loads can be issued ahead of the weight loads (vector
+ * memory results are consumed in issue order: an activation load issued
+ * after the weight ring would wait for all of it). Four consecutive
+ * threads share a chunk; a thread takes up to kXIt chunk quarters, which
+ * covers a slice of up to kXIt * 512 / 4 = 512 chunk-tokens. */
+constexpr int kXIt = 4;
+constexpr uint32_t kMaxSliceTok = (uint32_t)kXIt * 64u * kWaves / 4u;
+
 template <int MT>
-static int pick_rows(uint32_t n, uint32_t waves_per_wg) {
-  int best = 4;
-  for (int u = 8; u <= 16 / MT; u *= 2) {
-    const uint64_t waves = (uint64_t)((n + (uint32_t)u - 1u) / (uint32_t)u) * waves_per_wg;
-    if (waves >= 2048u) best = u;
+__device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, uint32_t ntok,
+                                       uint32_t cs, uint32_t nsc, float4 (&va)[kXIt],
+                                       float4 (&vb)[kXIt]) {
+  const uint32_t total = (uint32_t)MT * nsc * 4u;
+#pragma unroll
+  for (int it = 0; it < kXIt; ++it) {
+    const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
+    const uint32_t t = idx / (nsc * 4u), r = idx % (nsc * 4u);
+    /* clamped, unconditional load; tokens >= ntok and idle threads read
+     * token 0's first columns and are zeroed by the select below */
+    const bool ok = idx < total && t < ntok;
+    const float4 *src = reinterpret_cast<const float4 *>(
+        x + (ok ? (size_t)t * k + 32u * (cs + (r >> 2)) + 8u * (r & 3u) : (size_t)32u * cs));
+    const float4 a = src[0], b = src[1];
+    va[it] = make_float4(ok ? a.x : 0.f, ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
+    vb[it] = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
   }
+}
+
+template <int MT>
+__device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[kXIt],
+                                         const float4 (&vb)[kXIt], XSlot *xp, XScale *xf) {
+  const uint32_t total = (uint32_t)MT * nsc * 4u;
+#pragma unroll
+  for (int it = 0; it < kXIt; ++it) {
+    const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
+    if (idx < total) { /* whole quads are in or out together */
+      const uint32_t t = idx / (nsc * 4u), r = idx % (nsc * 4u);
+      const float v[8] = {va[it].x, va[it].y, va[it].z, va[it].w,
+                          vb[it].x, vb[it].y, vb[it].z, vb[it].w};
+      plane_words(v, r & 3u, &xp[t * nsc + (r >> 2)], &xf[t * nsc + (r >> 2)]);
+    }
+  }
+}
+
+/* Weight loads of a block are issued for all its lanes and rows with
+ * addresses clamped into the matrix (lanes or rows past the end re-read
+ * valid data whose contribution is masked with a select), so a block is
+ * one straight run of loads; whole blocks past the wave's last one are
+ * not issued. Outputs are written without reading y (a load inside the
+ * loop would wait for every weight load in flight): accumulating launches
+ * add with a non-returning atomic (each output has one writer per launch,
+ * and launches on a stream run in order, so the result is the same as a
+ * read-add-write). */
+template <class F, int U, int MT>
+__global__ void __launch_bounds__(64 * kWaves) k_gemv(paik_qview_t v, const float *__restrict__ x,
+                                                      float *__restrict__ y, uint32_t ntok,
+                                                      uint32_t cs, uint32_t nsc, int accumulate) {
+  static_assert(U * MT <= 16, "at most 16 outputs per row group");
+  extern __shared__ uint4 smem[];
+  XSlot *xp = reinterpret_cast<XSlot *>(smem);
+  XScale *xf = reinterpret_cast<XScale *>(xp + (size_t)MT * nsc);
+
+  const uint32_t lane = threadIdx.x & 63u;
+  /* the wave index is uniform; reading it from lane 0 lets every row and
+   * block quantity below live in scalar registers */
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const uint64_t gw = (uint64_t)blockIdx.x * kWaves + (uint64_t)wave;
+  const uint64_t tw = (uint64_t)gridDim.x * kWaves;
+  const uint32_t r_beg = (uint32_t)(gw * v.n / tw), r_end = (uint32_t)((gw + 1u) * v.n / tw);
+  const uint32_t steps = (nsc + 63u) >> 6;
+  const uint32_t groups = (r_end - r_beg + (uint32_t)U - 1u) / (uint32_t)U;
+  const uint32_t nblk = groups * steps; /* wave-uniform; 0 for a wave without rows */
+  const uint32_t blk_last = nblk > 0u ? nblk - 1u : 0u;
+  const uint32_t row_last = r_end > r_beg ? r_end - 1u : min(r_beg, v.n - 1u);
+
+  const QRes res = make_qres(v);
+  auto load_block = [&](uint32_t b, typename F::Raw (&buf)[U]) {
+    const uint32_t bb = min(b, blk_last);
+    const uint32_t g = bb / steps, s = bb % steps;
+    const uint32_t cb = cs + 64u * s;                /* wave-uniform chunk base */
+    const uint32_t ln = min(lane, nsc - 1u - 64u * s); /* cb + ln stays in the slice */
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      buf[u] = F::bload(res, min(r_beg + g * (uint32_t)U + (uint32_t)u, row_last), cb, ln);
+  };
+
+  /* Activation loads first, then the ring of PD blocks (kInFlight
+   * row-chunks per lane); the planes are built while the ring is in
+   * flight. */
+  float4 xa[kXIt], xb[kXIt];
+  x_load<MT>(x, v.k, ntok, cs, nsc, xa, xb);
+  constexpr int PD = kInFlight / U;
+  typename F::Raw buf[PD][U];
+#pragma unroll
+  for (int p = 0; p < PD; ++p)
+    if ((uint32_t)p < nblk) load_block((uint32_t)p, buf[p]);
+
+  x_planes<MT>(nsc, xa, xb, xp, xf);
+  __syncthreads();
+
+  float acc[U][MT];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[u][t] = 0.0f;
+
+  auto compute_block = [&](uint32_t b, const typename F::Raw (&buf)[U]) {
+    const uint32_t g = b / steps, s = b % steps;
+    const uint32_t cl = 64u * s + lane;
+    const bool live = cl < nsc;
+    const uint32_t clc = min(cl, nsc - 1u);
+    const uint32_t row0 = r_beg + g * (uint32_t)U;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      XChunk xc;
+      const XSlot &sl = xp[(uint32_t)t * nsc + clc];
+#pragma unroll
+      for (int p = 0; p < 6; ++p) {
+        const uint4 q = sl.X[p];
+        xc.X[p][0] = q.x;
+        xc.X[p][1] = q.y;
+        xc.X[p][2] = q.z;
+        xc.X[p][3] = q.w;
+      }
+      const XScale f = xf[(uint32_t)t * nsc + clc];
+      xc.xs = f.xs;
+      xc.sx0 = f.sx0;
+      xc.sx1 = f.sx1;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float d = F::dot(buf[u], cs + clc, xc);
+        acc[u][t] += (live && row0 + (uint32_t)u < r_end) ? d : 0.0f;
+      }
+    }
+    if (s + 1u == steps) {
+      /* Row group done: every output's 64 lane partials are summed in
+       * registers (DPP within 16-lane rows, then two cross-row steps); lane
+       * j then writes output j = u*MT + t. */
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const float sum = group_sum<64>(acc[u][t]);
+          acc[u][t] = 0.0f;
+          const uint32_t row = row0 + (uint32_t)u;
+          if (lane == (uint32_t)(u * MT + t) && row < r_end && (uint32_t)t < ntok) {
+            float *dst = y + (size_t)t * v.n + row;
+            if (accumulate) unsafeAtomicAdd(dst, sum);
+            else *dst = sum;
+          }
+        }
+    }
+  };
+
+  for (uint32_t b0 = 0; b0 < nblk; b0 += (uint32_t)PD) {
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+      const uint32_t b = b0 + (uint32_t)p;
+      if (b < nblk) {
+        compute_block(b, buf[p]);
+        /* a refill past the wave's last block would still have to return
+         * before the wave can retire */
+        if (b + (uint32_t)PD < nblk) load_block(b + (uint32_t)PD, buf[p]);
+      }
+    }
+  }
+}
+
+/* Workgroups: one per CU (256), fewer when that would leave waves with
+ * under two rows (a one-row group re-reads the activation planes for a
+ * single row). Rows per group U: 4 when waves get four or more rows, else
+ * 2 (U*MT <= 8). PAI_GEMV_WGS / PAI_GEMV_ROWS override both (tuning). */
+static uint32_t pick_grid(uint32_t n) {
+  uint32_t g = (n + 2u * kWaves - 1u) / (2u * kWaves);
+  if (g > 256u) g = 256u;
+  if (const char *e = getenv("PAI_GEMV_WGS")) {
+    const int r = atoi(e);
+    if (r >= 1 && r <= 65535) g = (uint32_t)r;
+  }
+  const uint32_t need = (n + kWaves - 1u) / kWaves; /* at least one row per wave */
+  return need < g ? need : g;
+}
+
+template <int MT>
+static int pick_rows(uint32_t n, uint32_t grid) {
+  const uint32_t rw = (n + grid * kWaves - 1u) / (grid * kWaves);
+  int u = (rw >= 4u && 4 * MT <= 8) ? 4 : (2 * MT <= 8 ? 2 : 1);
   if (const char *e = getenv("PAI_GEMV_ROWS")) {
     const int r = atoi(e);
-    if ((r == 4 || r == 8 || r == 16) && r * MT <= 16) best = r;
+    if ((r == 1 || r == 2 || r == 4) && r * MT <= 8) u = r;
   }
-  return best;
+  return u;
 }
 
 template <class F, int U, int MT>
 static hipError_t launch_u(const paik_qview_t &v, const float *x, float *y, uint32_t ntok,
-                           uint32_t waves, hipStream_t s) {
-  const dim3 grid((v.n + U - 1u) / U), block(64u * waves);
-  k_gemv<F, U, MT><<<grid, block, 0, s>>>(v, x, y, ntok);
-  return hipGetLastError();
+                           uint32_t grid, hipStream_t s) {
+  const uint32_t nchunks = v.k >> 5;
+  const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)MT * (sizeof(XSlot) + sizeof(XScale))));
+  const uint32_t cap = min(fit, kMaxSliceTok / (uint32_t)MT);
+  const uint32_t slice = cap >= nchunks ? nchunks : (cap & ~63u);
+  for (uint32_t cs = 0; cs < nchunks; cs += slice) {
+    const uint32_t nsc = min(slice, nchunks - cs);
+    const size_t lds = (size_t)MT * nsc * (sizeof(XSlot) + sizeof(XScale));
+    k_gemv<F, U, MT><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(v, x, y, ntok, cs, nsc,
+                                                                 cs != 0u ? 1 : 0);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <class F, int MT>
 static hipError_t launch_gemv(const paik_qview_t &v, const float *x, float *y, uint32_t ntok,
                               hipStream_t s) {
-  const uint32_t nseg = ((v.k >> 5) + 63u) >> 6;
-  const uint32_t waves = nseg < (uint32_t)kMaxWaves ? nseg : (uint32_t)kMaxWaves;
-  const int u = pick_rows<MT>(v.n, waves);
+  const uint32_t grid = pick_grid(v.n);
+  const int u = pick_rows<MT>(v.n, grid);
   if constexpr (MT == 1) {
-    if (u == 16) return launch_u<F, 16, 1>(v, x, y, ntok, waves, s);
-    if (u == 8) return launch_u<F, 8, 1>(v, x, y, ntok, waves, s);
-    return launch_u<F, 4, 1>(v, x, y, ntok, waves, s);
+    if (u == 4) return launch_u<F, 4, 1>(v, x, y, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 1>(v, x, y, ntok, grid, s);
+    return launch_u<F, 1, 1>(v, x, y, ntok, grid, s);
   } else if constexpr (MT == 2) {
-    if (u == 8) return launch_u<F, 8, 2>(v, x, y, ntok, waves, s);
-    return launch_u<F, 4, 2>(v, x, y, ntok, waves, s);
+    if (u == 4) return launch_u<F, 4, 2>(v, x, y, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 2>(v, x, y, ntok, grid, s);
+    return launch_u<F, 1, 2>(v, x, y, ntok, grid, s);
   } else {
-    return launch_u<F, 4, MT>(v, x, y, ntok, waves, s);
+    if (u == 2) return launch_u<F, 2, MT>(v, x, y, ntok, grid, s);
+    return launch_u<F, 1, MT>(v, x, y, ntok, grid, s);
   }
 }
 

@@ -14,8 +14,16 @@
 
 namespace paik {
 
+/* 16 bytes of nibble words from 32 per-column 4-bit fields f[0..31]:
+ * byte m of word j = f[8j+m] | f[8j+m+4] << 4. */
+__device__ void put_nibbles(uint8_t *dst, const uint8_t f[32]) {
+  for (int j = 0; j < 4; ++j)
+    for (int m = 0; m < 4; ++m)
+      dst[4 * j + m] = (uint8_t)((f[8 * j + m] & 0x0Fu) | ((f[8 * j + m + 4] & 0x0Fu) << 4));
+}
+
 /* One thread per chunk (32 columns of a row): gather its codes from the
- * native block into the chunk order of qdev.h; the first chunk of a block
+ * native block into the nibble words of qdev.h; the first chunk of a block
  * also copies the block's scales. */
 template <uint32_t T>
 __global__ void __launch_bounds__(256) k_repack(paik_qview_t v, const uint8_t *__restrict__ src) {
@@ -25,24 +33,30 @@ __global__ void __launch_bounds__(256) k_repack(paik_qview_t v, const uint8_t *_
   const size_t row = job / nc;
   const uint32_t c = (uint32_t)(job % nc);
   uint8_t *q = const_cast<uint8_t *>(v.q) + row * v.q_stride;
+  uint8_t f[32];
   if constexpr (T == 8u) { /* Q8_0 block: d | qs[32]; chunk = block */
     const uint8_t *s = src + (row * v.nb + c) * 34u;
     const_cast<uint16_t *>(v.d)[row * v.nb + c] = (uint16_t)(s[0] | (s[1] << 8));
-    for (int i = 0; i < 32; ++i) q[32u * c + i] = s[2 + i];
+    for (int k = 0; k < 32; ++k) f[k] = (uint8_t)((s[2 + k] & 0x0Fu) ^ 8u);
+    put_nibbles(q + 32u * c, f);
+    for (int k = 0; k < 32; ++k) f[k] = (uint8_t)(s[2 + k] >> 4);
+    put_nibbles(q + 32u * c + 16u, f);
   } else if constexpr (T == 2u) { /* Q4_0 block: d | qs[16]; chunk = block */
     const uint8_t *s = src + (row * v.nb + c) * 18u;
     const_cast<uint16_t *>(v.d)[row * v.nb + c] = (uint16_t)(s[0] | (s[1] << 8));
-    for (int i = 0; i < 16; ++i) q[16u * c + i] = s[2 + i];
+    for (int k = 0; k < 16; ++k) {
+      f[k] = (uint8_t)((s[2 + k] & 0x0Fu) ^ 8u);
+      f[16 + k] = (uint8_t)((s[2 + k] >> 4) ^ 8u);
+    }
+    put_nibbles(q + 16u * c, f);
   } else if constexpr (T == 12u) { /* Q4_K block: head[16] | qs[128] */
     const uint32_t b = c >> 3, j = c & 7u, p = j >> 1;
     const uint8_t *s = src + (row * v.nb + b) * 144u;
     const uint8_t *qs = s + 16 + 32u * p;
     /* sub-block 2p: low nibbles of qs[32p + l]; 2p+1: high nibbles */
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t a = qs[i], e = qs[16 + i];
-      q[16u * c + i] = (j & 1u) ? (uint8_t)((a >> 4) | (e & 0xF0u))
-                                : (uint8_t)((a & 0x0Fu) | ((e & 0x0Fu) << 4));
-    }
+    for (int l = 0; l < 32; ++l)
+      f[l] = (uint8_t)(((j & 1u) ? (qs[l] >> 4) : (qs[l] & 0x0Fu)) ^ 8u);
+    put_nibbles(q + 16u * c, f);
     if (j == 0u) {
       uint8_t *m = const_cast<uint8_t *>(v.meta) + (row * v.nb + b) * 16u;
       for (int i = 0; i < 16; ++i) m[i] = s[i];
@@ -52,19 +66,19 @@ __global__ void __launch_bounds__(256) k_repack(paik_qview_t v, const uint8_t *_
     const uint8_t *s = src + (row * v.nb + b) * 210u;
     const uint8_t *ql = s + 64u * h + ((g & 1u) ? 32u : 0u);
     const uint8_t *qh = s + 128u + 32u * h;
-    uint8_t lo4[32], hi2[32];
+    uint8_t hi2[32];
     for (int l = 0; l < 32; ++l) {
-      lo4[l] = (g & 2u) ? (uint8_t)(ql[l] >> 4) : (uint8_t)(ql[l] & 0x0Fu);
+      f[l] = (uint8_t)(((g & 2u) ? (ql[l] >> 4) : (ql[l] & 0x0Fu)) ^ 8u);
       hi2[l] = (uint8_t)((qh[l] >> (2u * g)) & 3u);
     }
-    for (int i = 0; i < 16; ++i) q[16u * c + i] = (uint8_t)(lo4[i] | (lo4[16 + i] << 4));
+    put_nibbles(q + 16u * c, f);
     uint8_t *e = const_cast<uint8_t *>(v.aux) + row * (v.k >> 2) + 8u * c;
     for (int t = 0; t < 2; ++t) {
-      for (int by = 0; by < 4; ++by) {
-        uint32_t acc = 0;
-        for (int k = 0; k < 4; ++k) acc |= (uint32_t)hi2[16 * t + 4 * k + by] << (2 * k);
-        e[4 * t + by] = (uint8_t)acc;
-      }
+      uint32_t w = 0;
+      for (int i = 0; i < 8; ++i)
+        w |= ((uint32_t)hi2[16 * t + i] << nib_off(i)) |
+             ((uint32_t)hi2[16 * t + 8 + i] << (nib_off(i) + 2));
+      for (int by = 0; by < 4; ++by) e[4 * t + by] = (uint8_t)(w >> (8 * by));
     }
     if (j == 0u) {
       uint8_t *m = const_cast<uint8_t *>(v.meta) + (row * v.nb + b) * 16u;
