@@ -3,14 +3,16 @@
 
 Headline (the JSON `value`): Q4_0 decode GEMV, M=1, over the seven
 Llama-3-8B per-layer projections (q, o: 4096x4096; k, v: 1024x4096;
-gate, up: 14336x4096; down: 4096x14336). One step = the seven projections
-of one layer on one activation vector; steps rotate over --layers distinct
-weight copies so the working set (123 MB per layer) exceeds the 256 MB
-Infinity Cache. Weights are f32 N(0, 0.02^2) from a fixed seed, quantized
-by libpai_hip's encoder; activations are f32 N(0, 1), resident in HBM.
+gate, up: 14336x4096; down: 4096x14336), issued as one layer's decode step:
+q/k/v in one fused call (they share the attention input), o, gate/up in one
+fused call (they share the FFN input), down -- four launches streaming the
+seven matrices. Steps rotate over --layers distinct weight copies so the
+working set (123 MB per layer) exceeds the 256 MB Infinity Cache. Weights
+are f32 N(0, 0.02^2) from a fixed seed, quantized by libpai_hip's encoder;
+activations are f32 N(0, 1), resident in HBM.
 
 value    = algorithmic bytes (packed W + x + y, f32) of all timed steps
-           / wall time between two device synchronisations.
+           / wall time between two stream synchronisations.
 roofline = the GEMV kernel: the same bytes / the sum of its launch
            durations (HIP events around every launch, on the launch stream),
            against 8 TB/s.
@@ -18,9 +20,9 @@ cpu_baseline = the reference's AVX2+FMA GEMV (cpu/optimized/opt_ops.c,
            compiled from its sources into oracle/_ref; this repository's
            restatement when that build is absent) on the dequantized f32
            weights of the same seven projections, one host core.
-extra    = the other configurations: Q8_0 4096x4096 GEMV, Q4_K GEMV at
-           M in {1, 8, 32}, and the M=512 prefill GEMMs (gate Q4_K,
-           down Q6_K) in TFLOP/s against 2.5 PFLOP/s dense fp16.
+extra    = the seven projections as separate launches, Q4_K at M in
+           {1, 8, 32}, Q8_0 4096x4096 GEMV, and the M=512 prefill GEMMs
+           (gate Q4_K, down Q6_K) in TFLOP/s against 2.5 PFLOP/s dense fp16.
 """
 from __future__ import annotations
 
@@ -59,6 +61,7 @@ class Layer:
     """One layer's seven packed projections on the device."""
 
     def __init__(self, pa, qtype: int, blocks: list):
+        self.qtype = qtype
         self.w = [pa.QMat(qtype, n, k, b) for (_, n, k), b in zip(PROJ, blocks)]
 
 
@@ -70,70 +73,102 @@ def quantized_layer(pa, qtype: int, config: int) -> list:
     return out
 
 
-def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, per_launch_events: bool):
-    """Time `steps` passes over the seven projections, rotating layers.
-    Every launch goes to one HIP stream; the per-launch events are recorded
-    on that stream."""
+# The launches of one layer's decode step: projections that share their
+# input run as one fused call (q/k/v on the attention input, gate/up on the
+# FFN input); o and down stand alone.
+FUSED_STEP = [("qkv", [0, 1, 2]), ("o", [3]), ("gate_up", [4, 5]), ("down", [6])]
+SEPARATE_STEP = [(name, [i]) for i, (name, _, _) in enumerate(PROJ)]
+
+
+def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, plan):
+    """Time `steps` passes over the seven projections, rotating layers. Each
+    layer copy's pass (the launches of `plan`) is captured once into a HIP
+    graph; a step is one graph replay on one stream. The timed region is
+    bracketed by events on that stream, so the GPU time per step is the
+    kernels' time plus the gaps between them inside the graph."""
     stream = hm.Stream()
-    sh = stream.handle
     kmax = max(k for _, _, k in PROJ)
     x = hm.DeviceBuffer.from_array(pa.normal_f32(0xC0DE0000 ^ 0x5A5A, m * kmax))
     ys = [hm.DeviceBuffer(m * n * 4) for _, n, _ in PROJ]
     xp, yp = x.ptr, [y.ptr for y in ys]
 
-    def step(s, evs=None):
-        layer = layers[s % len(layers)]
-        for j, w in enumerate(layer.w):
-            if evs is not None:
-                evs[2 * j].record(stream)
-            w.gemm_async(xp, yp[j], m, 0, sh)
-            if evs is not None:
-                evs[2 * j + 1].record(stream)
+    def enqueue(layer, sh):
+        for _, idx in plan:
+            if len(idx) == 1:
+                layer.w[idx[0]].gemm_async(xp, yp[idx[0]], m, 0, sh)
+            else:
+                pa.gemm_multi_async([layer.w[i] for i in idx], xp, [yp[i] for i in idx], m, 0, sh)
 
+    graphs = [hm.Graph(stream, lambda sh, l=l: enqueue(l, sh)) for l in layers]
     for s in range(warmup):
-        step(s)
-    evs = None
-    if per_launch_events:
-        evs = [[hm.Event() for _ in range(2 * len(PROJ))] for _ in range(steps)]
+        graphs[s % len(graphs)].launch(stream)
     stream.synchronize()
+    a, b = hm.Event(), hm.Event()
     t0 = time.perf_counter()
+    a.record(stream)
     for s in range(steps):
-        step(s, evs[s] if evs else None)
+        graphs[s % len(graphs)].launch(stream)
+    b.record(stream)
     stream.synchronize()
     wall = time.perf_counter() - t0
-    per_proj_ms = None
-    if evs:
-        per_proj_ms = np.zeros(len(PROJ))
-        for e in evs:
-            for j in range(len(PROJ)):
-                per_proj_ms[j] += e[2 * j].elapsed_ms(e[2 * j + 1])
-        per_proj_ms /= steps
-        for e in evs:
-            for ev in e:
-                ev.destroy()
-    for b in [x, *ys]:
-        b.free()
+    gpu_ms = a.elapsed_ms(b)
+    for g in graphs:
+        g.destroy()
+    a.destroy(); b.destroy()
+    for buf in [x, *ys]:
+        buf.free()
     stream.destroy()
-    return wall, per_proj_ms
+    return wall, gpu_ms / steps
+
+
+def per_launch_times(pa, hm, layers, m: int, plan, reps: int = 50) -> dict:
+    """Microseconds per launch of each entry of `plan` (events around `reps`
+    back-to-back launches of that entry, rotating layers, on one stream)."""
+    stream = hm.Stream()
+    kmax = max(k for _, _, k in PROJ)
+    x = hm.DeviceBuffer.from_array(pa.normal_f32(0xC0DE0000 ^ 0x5A5A, m * kmax))
+    ys = [hm.DeviceBuffer(m * n * 4) for _, n, _ in PROJ]
+    out = {}
+    for name, idx in plan:
+        def one(sh, r):
+            layer = layers[r % len(layers)]
+            if len(idx) == 1:
+                layer.w[idx[0]].gemm_async(x.ptr, ys[idx[0]].ptr, m, 0, sh)
+            else:
+                pa.gemm_multi_async([layer.w[i] for i in idx], x.ptr, [ys[i].ptr for i in idx],
+                                    m, 0, sh)
+        g = hm.Graph(stream, lambda sh: [one(sh, r) for r in range(reps)])
+        g.launch(stream)
+        stream.synchronize()
+        a, b = hm.Event(), hm.Event()
+        a.record(stream)
+        g.launch(stream)
+        b.record(stream)
+        b.synchronize()
+        us = a.elapsed_ms(b) * 1e3 / reps
+        nbytes = sum(call_bytes(pa, layers[0].qtype, PROJ[i][1], PROJ[i][2], m) for i in idx)
+        out[name] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        a.destroy(); b.destroy(); g.destroy()
+    for buf in [x, *ys]:
+        buf.free()
+    stream.destroy()
+    return out
 
 
 def gemv_config(pa, hm, qtype: int, config: int, m: int, nlayers: int, steps: int,
-                warmup: int, per_launch_events: bool = True) -> dict:
+                warmup: int, plan=FUSED_STEP, launch_detail: bool = True) -> dict:
     blocks = quantized_layer(pa, qtype, config)
     layers = [Layer(pa, qtype, blocks) for _ in range(nlayers)]
-    wall, per_ms = run_layers(pa, hm, layers, m, steps, warmup, per_launch_events)
+    wall, gpu_ms = run_layers(pa, hm, layers, m, steps, warmup, plan)
     bytes_step = sum(call_bytes(pa, qtype, n, k, m) for _, n, k in PROJ)
     res = {"qtype": qtype, "m": m, "layers": nlayers, "steps": steps,
+           "launches_per_step": len(plan),
            "weight_set_MB": round(nlayers * sum(l.nbytes for l in layers[0].w) / 1e6, 1),
            "bytes_per_step": bytes_step, "ms_per_step": wall / steps * 1e3,
-           "GBps": bytes_step * steps / wall / 1e9}
-    if per_ms is not None:
-        kern_ms = float(per_ms.sum())
-        res["kernel_GBps"] = bytes_step / (kern_ms * 1e-3) / 1e9
-        res["per_projection"] = {
-            name: {"us": round(float(t) * 1e3, 2),
-                   "GBps": round(call_bytes(pa, qtype, n, k, m) / (t * 1e-3) / 1e9, 1)}
-            for (name, n, k), t in zip(PROJ, per_ms)}
+           "GBps": bytes_step * steps / wall / 1e9,
+           "gpu_ms_per_step": gpu_ms, "gpu_GBps": bytes_step / (gpu_ms * 1e-3) / 1e9}
+    if launch_detail:
+        res["per_launch"] = per_launch_times(pa, hm, layers, m, plan)
     for l in layers:
         for w in l.w:
             w.free()
@@ -141,19 +176,21 @@ def gemv_config(pa, hm, qtype: int, config: int, m: int, nlayers: int, steps: in
 
 
 def timed_calls(hm, call, reps: int, warm: int) -> float:
-    """Mean microseconds per call of `call(stream_handle, i)` between two
-    events on one stream."""
+    """Mean microseconds per call of `call(stream_handle, i)`: `reps` calls
+    captured into one HIP graph, replayed between two events on one
+    stream."""
     st = hm.Stream()
-    for i in range(warm):
-        call(st.handle, i)
+    warm_g = hm.Graph(st, lambda sh: [call(sh, i) for i in range(warm)])
+    g = hm.Graph(st, lambda sh: [call(sh, i) for i in range(reps)])
+    warm_g.launch(st)
+    st.synchronize()
     a, b = hm.Event(), hm.Event()
     a.record(st)
-    for i in range(reps):
-        call(st.handle, i)
+    g.launch(st)
     b.record(st)
     b.synchronize()
     us = a.elapsed_ms(b) / reps * 1e3
-    a.destroy(); b.destroy(); st.destroy()
+    a.destroy(); b.destroy(); g.destroy(); warm_g.destroy(); st.destroy()
     return us
 
 
@@ -264,13 +301,15 @@ def main() -> int:
     log(f"Q4_0 M=1 x {args.layers} layers")
 
     head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup)
-    log(f"Q4_0 M=1: {head['GBps']:.1f} GB/s wall, {head.get('kernel_GBps', 0):.1f} GB/s kernels")
-    roof = {"bound": "hbm", "achieved": round(head["kernel_GBps"], 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(head["kernel_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": "paik::k_gemv<Q4_0,1>",
-            "bytes_per_launch": round(head["bytes_per_step"] / len(PROJ)),
-            "avg_launch_us": round(head["bytes_per_step"] / len(PROJ)
-                                   / (head["kernel_GBps"] * 1e9) * 1e6, 3)}
+    log(f"Q4_0 M=1 fused step: {head['GBps']:.1f} GB/s wall, {head['gpu_GBps']:.1f} GB/s GPU; "
+        f"{head['per_launch']}")
+    avg_us = head["gpu_ms_per_step"] * 1e3 / head["launches_per_step"]
+    roof = {"bound": "hbm", "achieved": round(head["gpu_GBps"], 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(head["gpu_GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": None, "kernel": "paik::k_gemv<paik::Q4_0, U, 1>",
+            "launches_per_step": head["launches_per_step"],
+            "bytes_per_launch": round(head["bytes_per_step"] / head["launches_per_step"]),
+            "avg_launch_us": round(avg_us, 3)}
     traffic_file = ROOT / "profiles" / "traffic_gemv_q4_0.json"
     if traffic_file.exists():
         roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
@@ -278,12 +317,15 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         try:
+            extra["q4_0_m1_separate"] = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, 300, 20,
+                                                    plan=SEPARATE_STEP)
+            log(f"Q4_0 M=1 separate: {extra['q4_0_m1_separate']['gpu_GBps']:.1f} GB/s GPU")
             extra["q4_k_m1"] = gemv_config(pa, hm, pa.Q4_K, 3, 1, args.layers, 300, 20)
-            log(f"Q4_K M=1: {extra['q4_k_m1']['kernel_GBps']:.1f} GB/s kernels")
+            log(f"Q4_K M=1: {extra['q4_k_m1']['gpu_GBps']:.1f} GB/s GPU; "
+                f"{extra['q4_k_m1']['per_launch']}")
             for m in (8, 32):
-                extra[f"q4_k_m{m}"] = gemv_config(pa, hm, pa.Q4_K, 3, m, args.layers, 100, 5,
-                                                  per_launch_events=False)
-                log(f"Q4_K M={m}: {extra[f'q4_k_m{m}']['GBps']:.1f} GB/s")
+                extra[f"q4_k_m{m}"] = gemv_config(pa, hm, pa.Q4_K, 3, m, args.layers, 100, 5)
+                log(f"Q4_K M={m}: {extra[f'q4_k_m{m}']['gpu_GBps']:.1f} GB/s GPU")
             extra["q8_0_4096x4096_m1"] = q8_config1(pa, hm, 300)
             extra["prefill_m512"] = prefill(pa, hm, 20)
             log(f"prefill: {extra['prefill_m512']}")
@@ -303,12 +345,13 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "Q4_0 GEMV M=1, Llama-3-8B projections q,k,v,o,gate,up,down "
-                               f"(one layer per step, {args.layers} rotating layer copies)",
+                               "as one layer's decode step (q/k/v fused, o, gate/up fused, "
+                               f"down: 4 launches), {args.layers} rotating layer copies",
                    "weights": "Q4_0 (18 B / 32), f32 N(0,0.02^2) seeded, libpai_hip encoder",
                    "activations": "f32 N(0,1) resident in HBM",
                    "weight_set_MB": head["weight_set_MB"],
                    "frac_hbm_wall": round(head["GBps"] / HBM_PEAK_GBS, 4),
-                   "per_projection": head.get("per_projection")},
+                   "per_launch": head.get("per_launch")},
         "roofline": roof,
         "cpu_baseline": cpu,
         "extra": extra,

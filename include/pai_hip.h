@@ -145,6 +145,24 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
                                  const float *x, float *y, uint32_t flags,
                                  void *stream);
 
+/* Fused projections: y_i[m][N_i] = x[m][K] * W_i^T for `count` (1..4)
+ * matrices that share the activations (the q/k/v or gate/up projections
+ * of one layer). All matrices must have the same type and K (otherwise
+ * PAI_ERR_MISMATCH). x and every y_i are device pointers; `stream` is a
+ * hipStream_t (NULL = the default stream); the call returns once the
+ * kernels are enqueued. For M < 32 (or PAI_QGEMM_FP32) the matrices are
+ * multiplied in one launch per group of up to 4 tokens, which streams all
+ * of their blocks and converts x once; results are bit-identical to
+ * separate pai_qgemm_f32_async calls. For M >= 32 each matrix takes the
+ * MFMA path of pai_qgemm_f32_async.
+ * No counterpart in the reference, whose executor runs each projection as
+ * its own pai_ref_gemm_f32 (scheduler/scheduler.c:340); this is the fused
+ * form of those calls for weights that share an input value
+ * (adapters/llama/llama.c:678-696, :760-772). */
+pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t count,
+                                       uint64_t m, const float *x, float *const *ys,
+                                       uint32_t flags, void *stream);
+
 /* out[N][K] = dequantized W in the native element order, computed on the
  * GPU from the device copy; bit-identical to pai_gguf_dequant
  * (adapters/llama/gguf.c:650-967) for every row. Host pointer unless

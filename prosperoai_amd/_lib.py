@@ -34,6 +34,8 @@ SIGNATURES = {
     "pai_qmat_bytes": (C.c_uint64, [_vp]),
     "pai_qgemm_f32": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32]),
     "pai_qgemm_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32, _vp]),
+    "pai_qgemm_f32_multi_async": (C.c_int32, [C.POINTER(C.c_void_p), C.c_uint32, C.c_uint64, _vp,
+                                              C.POINTER(C.c_void_p), C.c_uint32, _vp]),
     "pai_qdequant_f32": (C.c_int32, [_vp, _vp, C.c_uint32]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),
     "pai_hip_op_name": (C.c_char_p, [C.c_uint32]),

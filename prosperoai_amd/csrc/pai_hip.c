@@ -347,6 +347,36 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m, const float *x
   return launch(w, m, x, y, flags, (hipStream_t)stream);
 }
 
+#define PAI_MULTI_MAX 4u
+
+pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t count, uint64_t m,
+                                       const float *x, float *const *ys, uint32_t flags,
+                                       void *stream) {
+  if (ws == NULL || ys == NULL || x == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  if (count == 0u || count > PAI_MULTI_MAX)
+    return fail(PAI_ERR_INVALID_ARG, "count=%u, expected 1..%u", count, PAI_MULTI_MAX);
+  for (uint32_t i = 0; i < count; ++i) {
+    pai_status_t st = check_call(ws[i], m, x, ys[i]);
+    if (st != PAI_OK) return st;
+    if (((uintptr_t)ys[i] & 3u) != 0u) return fail(PAI_ERR_INVALID_ARG, "y must be 4-byte aligned");
+    if (ws[i]->type != ws[0]->type || ws[i]->k != ws[0]->k)
+      return fail(PAI_ERR_MISMATCH, "matrix %u differs from matrix 0 in type or K", i);
+  }
+  if (((uintptr_t)x & 15u) != 0u) return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
+    const paik_qview_t *vs[PAI_MULTI_MAX];
+    for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
+    const int e = paik_gemv_multi(vs, ys, count, (uint32_t)m, x, s);
+    return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+  }
+  for (uint32_t i = 0; i < count; ++i) {
+    pai_status_t st = launch(ws[i], m, x, ys[i], flags, s);
+    if (st != PAI_OK) return st;
+  }
+  return PAI_OK;
+}
+
 pai_status_t pai_qgemm_f32(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
                            uint32_t flags) {
   pai_status_t st = check_call(w, m, x, y);

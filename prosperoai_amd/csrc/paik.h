@@ -56,6 +56,10 @@ int paik_repack(const paik_qview_t *v, const uint8_t *native, void *stream);
 int paik_dequant(const paik_qview_t *v, float *out, void *stream);
 int paik_gemv(const paik_qview_t *v, uint32_t m, const float *x, float *y,
               void *stream);
+/* y_i = x * W_i^T for count (1..4) matrices of one format and column
+ * count, in one launch per group of up to 4 tokens. */
+int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys,
+                    uint32_t count, uint32_t m, const float *x, void *stream);
 int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
                    float *y, int bf16, void *stream);
 

@@ -35,6 +35,8 @@
  * (<= 2^-23 of the chunk's largest |x|), the per-chunk scale steps and the
  * f32 additions across chunks and lanes.
  */
+#include <string.h>
+
 #include "qdev.h"
 
 namespace paik {
@@ -175,6 +177,18 @@ __device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[kXIt],
   }
 }
 
+/* Matrices of one launch: up to kMaxMats weights with the same format and
+ * column count, multiplied by the same activations (the q/k/v or gate/up
+ * projections of a layer). Waves [wave_end[i-1], wave_end[i]) work on
+ * matrix i, so no wave's rows cross a matrix boundary. */
+constexpr int kMaxMats = 4;
+struct GemvArgs {
+  paik_qview_t v[kMaxMats];
+  float *y[kMaxMats];
+  uint32_t wave_end[kMaxMats];
+  uint32_t count;
+};
+
 /* Weight loads of a block are issued for all its lanes and rows with
  * addresses clamped into the matrix (lanes or rows past the end re-read
  * valid data whose contribution is masked with a select), so a block is
@@ -185,9 +199,9 @@ __device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[kXIt],
  * and launches on a stream run in order, so the result is the same as a
  * read-add-write). */
 template <class F, int U, int MT>
-__global__ void __launch_bounds__(64 * kWaves) k_gemv(paik_qview_t v, const float *__restrict__ x,
-                                                      float *__restrict__ y, uint32_t ntok,
-                                                      uint32_t cs, uint32_t nsc, int accumulate) {
+__global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *__restrict__ x,
+                                                      uint32_t ntok, uint32_t cs, uint32_t nsc,
+                                                      int accumulate) {
   static_assert(U * MT <= 16, "at most 16 outputs per row group");
   extern __shared__ uint4 smem[];
   XSlot *xp = reinterpret_cast<XSlot *>(smem);
@@ -197,9 +211,25 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(paik_qview_t v, const floa
   /* the wave index is uniform; reading it from lane 0 lets every row and
    * block quantity below live in scalar registers */
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const uint64_t gw = (uint64_t)blockIdx.x * kWaves + (uint64_t)wave;
-  const uint64_t tw = (uint64_t)gridDim.x * kWaves;
-  const uint32_t r_beg = (uint32_t)(gw * v.n / tw), r_end = (uint32_t)((gw + 1u) * v.n / tw);
+  const uint32_t gw = blockIdx.x * (uint32_t)kWaves + wave;
+  /* the matrix this wave works on, and its share of that matrix's rows */
+  uint32_t mi = 0, w0 = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxMats; ++i)
+    if ((uint32_t)i < a.count && gw >= a.wave_end[i - 1]) {
+      mi = (uint32_t)i;
+      w0 = a.wave_end[i - 1];
+    }
+  paik_qview_t v = a.v[0];
+  float *y = a.y[0];
+#pragma unroll
+  for (int i = 1; i < kMaxMats; ++i)
+    if (mi == (uint32_t)i) {
+      v = a.v[i];
+      y = a.y[i];
+    }
+  const uint64_t lw = gw - w0, tw = a.wave_end[mi] - w0;
+  const uint32_t r_beg = (uint32_t)(lw * v.n / tw), r_end = (uint32_t)((lw + 1u) * v.n / tw);
   const uint32_t steps = (nsc + 63u) >> 6;
   const uint32_t groups = (r_end - r_beg + (uint32_t)U - 1u) / (uint32_t)U;
   const uint32_t nblk = groups * steps; /* wave-uniform; 0 for a wave without rows */
@@ -303,7 +333,7 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(paik_qview_t v, const floa
  * under two rows (a one-row group re-reads the activation planes for a
  * single row). Rows per group U: 4 when waves get four or more rows, else
  * 2 (U*MT <= 8). PAI_GEMV_WGS / PAI_GEMV_ROWS override both (tuning). */
-static uint32_t pick_grid(uint32_t n) {
+static uint32_t pick_grid(uint32_t n, uint32_t count) {
   uint32_t g = (n + 2u * kWaves - 1u) / (2u * kWaves);
   if (g > 256u) g = 256u;
   if (const char *e = getenv("PAI_GEMV_WGS")) {
@@ -311,7 +341,9 @@ static uint32_t pick_grid(uint32_t n) {
     if (r >= 1 && r <= 65535) g = (uint32_t)r;
   }
   const uint32_t need = (n + kWaves - 1u) / kWaves; /* at least one row per wave */
-  return need < g ? need : g;
+  if (need < g) g = need;
+  const uint32_t least = (count + kWaves - 1u) / kWaves; /* a wave per matrix */
+  return g < least ? least : g;
 }
 
 template <int MT>
@@ -325,17 +357,33 @@ static int pick_rows(uint32_t n, uint32_t grid) {
   return u;
 }
 
+/* Waves per matrix in proportion to its rows (at least one each). */
+static void split_waves(GemvArgs &a, uint32_t total_waves) {
+  uint64_t rows = 0;
+  for (uint32_t i = 0; i < a.count; ++i) rows += a.v[i].n;
+  uint32_t given = 0;
+  for (uint32_t i = 0; i < a.count; ++i) {
+    uint32_t w = (uint32_t)((uint64_t)total_waves * a.v[i].n / rows);
+    if (w < 1u) w = 1u;
+    const uint32_t left = total_waves - given - (a.count - 1u - i); /* keep one per later matrix */
+    if (w > left || i + 1u == a.count) w = left;
+    given += w;
+    a.wave_end[i] = given;
+  }
+}
+
 template <class F, int U, int MT>
-static hipError_t launch_u(const paik_qview_t &v, const float *x, float *y, uint32_t ntok,
-                           uint32_t grid, hipStream_t s) {
-  const uint32_t nchunks = v.k >> 5;
+static hipError_t launch_u(GemvArgs a, const float *x, uint32_t ntok, uint32_t grid,
+                           hipStream_t s) {
+  const uint32_t nchunks = a.v[0].k >> 5;
   const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)MT * (sizeof(XSlot) + sizeof(XScale))));
   const uint32_t cap = min(fit, kMaxSliceTok / (uint32_t)MT);
   const uint32_t slice = cap >= nchunks ? nchunks : (cap & ~63u);
+  split_waves(a, grid * (uint32_t)kWaves);
   for (uint32_t cs = 0; cs < nchunks; cs += slice) {
     const uint32_t nsc = min(slice, nchunks - cs);
     const size_t lds = (size_t)MT * nsc * (sizeof(XSlot) + sizeof(XScale));
-    k_gemv<F, U, MT><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(v, x, y, ntok, cs, nsc,
+    k_gemv<F, U, MT><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(a, x, ntok, cs, nsc,
                                                                  cs != 0u ? 1 : 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -344,36 +392,43 @@ static hipError_t launch_u(const paik_qview_t &v, const float *x, float *y, uint
 }
 
 template <class F, int MT>
-static hipError_t launch_gemv(const paik_qview_t &v, const float *x, float *y, uint32_t ntok,
-                              hipStream_t s) {
-  const uint32_t grid = pick_grid(v.n);
-  const int u = pick_rows<MT>(v.n, grid);
+static hipError_t launch_gemv(const GemvArgs &a, const float *x, uint32_t ntok, hipStream_t s) {
+  uint32_t rows = 0;
+  for (uint32_t i = 0; i < a.count; ++i) rows += a.v[i].n;
+  const uint32_t grid = pick_grid(rows, a.count);
+  const int u = pick_rows<MT>(rows, grid);
   if constexpr (MT == 1) {
-    if (u == 4) return launch_u<F, 4, 1>(v, x, y, ntok, grid, s);
-    if (u == 2) return launch_u<F, 2, 1>(v, x, y, ntok, grid, s);
-    return launch_u<F, 1, 1>(v, x, y, ntok, grid, s);
+    if (u == 4) return launch_u<F, 4, 1>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 1>(a, x, ntok, grid, s);
+    return launch_u<F, 1, 1>(a, x, ntok, grid, s);
   } else if constexpr (MT == 2) {
-    if (u == 4) return launch_u<F, 4, 2>(v, x, y, ntok, grid, s);
-    if (u == 2) return launch_u<F, 2, 2>(v, x, y, ntok, grid, s);
-    return launch_u<F, 1, 2>(v, x, y, ntok, grid, s);
+    if (u == 4) return launch_u<F, 4, 2>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 2>(a, x, ntok, grid, s);
+    return launch_u<F, 1, 2>(a, x, ntok, grid, s);
   } else {
-    if (u == 2) return launch_u<F, 2, MT>(v, x, y, ntok, grid, s);
-    return launch_u<F, 1, MT>(v, x, y, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, MT>(a, x, ntok, grid, s);
+    return launch_u<F, 1, MT>(a, x, ntok, grid, s);
   }
 }
 
 template <class F>
-static hipError_t gemv_tokens(const paik_qview_t &v, uint32_t m, const float *x, float *y,
-                              hipStream_t s) {
+static hipError_t gemv_tokens(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                              uint32_t m, const float *x, hipStream_t s) {
   /* groups of up to 4 tokens per launch; each launch re-streams W */
   for (uint32_t t0 = 0; t0 < m; t0 += 4u) {
     const uint32_t nt = m - t0 < 4u ? m - t0 : 4u;
-    const float *xt = x + (size_t)t0 * v.k;
-    float *yt = y + (size_t)t0 * v.n;
+    GemvArgs a;
+    memset(&a, 0, sizeof a);
+    a.count = count;
+    for (uint32_t i = 0; i < count; ++i) {
+      a.v[i] = *vs[i];
+      a.y[i] = ys[i] + (size_t)t0 * vs[i]->n;
+    }
+    const float *xt = x + (size_t)t0 * vs[0]->k;
     hipError_t e;
-    if (nt == 1u) e = launch_gemv<F, 1>(v, xt, yt, 1u, s);
-    else if (nt == 2u) e = launch_gemv<F, 2>(v, xt, yt, 2u, s);
-    else e = launch_gemv<F, 4>(v, xt, yt, nt, s);
+    if (nt == 1u) e = launch_gemv<F, 1>(a, xt, 1u, s);
+    else if (nt == 2u) e = launch_gemv<F, 2>(a, xt, 2u, s);
+    else e = launch_gemv<F, 4>(a, xt, nt, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -383,14 +438,20 @@ static hipError_t gemv_tokens(const paik_qview_t &v, uint32_t m, const float *x,
 
 using namespace paik;
 
-extern "C" int paik_gemv(const paik_qview_t *v, uint32_t m, const float *x, float *y,
-                         void *stream) {
+extern "C" int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                               uint32_t m, const float *x, void *stream) {
+  if (count == 0u || count > (uint32_t)kMaxMats) return (int)hipErrorInvalidValue;
   hipStream_t s = (hipStream_t)stream;
-  switch (v->type) {
-  case 8u: return (int)gemv_tokens<Q8_0>(*v, m, x, y, s);
-  case 2u: return (int)gemv_tokens<Q4_0>(*v, m, x, y, s);
-  case 12u: return (int)gemv_tokens<Q4_K>(*v, m, x, y, s);
-  case 14u: return (int)gemv_tokens<Q6_K>(*v, m, x, y, s);
+  switch (vs[0]->type) {
+  case 8u: return (int)gemv_tokens<Q8_0>(vs, ys, count, m, x, s);
+  case 2u: return (int)gemv_tokens<Q4_0>(vs, ys, count, m, x, s);
+  case 12u: return (int)gemv_tokens<Q4_K>(vs, ys, count, m, x, s);
+  case 14u: return (int)gemv_tokens<Q6_K>(vs, ys, count, m, x, s);
   default: return (int)hipErrorInvalidValue;
   }
+}
+
+extern "C" int paik_gemv(const paik_qview_t *v, uint32_t m, const float *x, float *y,
+                         void *stream) {
+  return paik_gemv_multi(&v, &y, 1u, m, x, stream);
 }

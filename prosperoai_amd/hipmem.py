@@ -42,6 +42,12 @@ def hip() -> C.CDLL:
             "hipEventSynchronize": [vp],
             "hipEventElapsedTime": [C.POINTER(C.c_float), vp, vp],
             "hipGetLastError": [],
+            "hipStreamBeginCapture": [vp, C.c_int],
+            "hipStreamEndCapture": [vp, C.POINTER(vp)],
+            "hipGraphInstantiate": [C.POINTER(vp), vp, vp, C.c_char_p, C.c_size_t],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp],
         }
         for name, args in sigs.items():
             fn = getattr(h, name)
@@ -146,3 +152,32 @@ class Event:
 
 def synchronize() -> None:
     hip_check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Graph:
+    """A HIP graph captured from the work `fn(stream_handle)` enqueues on a
+    stream (hipStreamBeginCapture ... hipStreamEndCapture), instantiated
+    once and replayed with one host call."""
+
+    def __init__(self, stream: Stream, fn):
+        g = C.c_void_p()
+        hip_check(hip().hipStreamBeginCapture(stream._s, 1), "hipStreamBeginCapture")  # thread-local
+        try:
+            fn(stream.handle)
+        finally:
+            hip_check(hip().hipStreamEndCapture(stream._s, C.byref(g)), "hipStreamEndCapture")
+        self._g = g
+        self._e = C.c_void_p()
+        hip_check(hip().hipGraphInstantiate(C.byref(self._e), g, None, None, 0),
+                  "hipGraphInstantiate")
+
+    def launch(self, stream: Stream) -> None:
+        hip_check(hip().hipGraphLaunch(self._e, stream._s), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        if self._e.value:
+            hip().hipGraphExecDestroy(self._e)
+            self._e = C.c_void_p()
+        if self._g.value:
+            hip().hipGraphDestroy(self._g)
+            self._g = C.c_void_p()

@@ -110,3 +110,14 @@ class QMat:
     def gemm_async(self, x_ptr: int, y_ptr: int, m: int, flags: int = 0, stream: int = 0) -> None:
         check(lib().pai_qgemm_f32_async(self._h, m, x_ptr, y_ptr, flags | FLAG_DEVICE_PTRS,
                                         stream or None), "pai_qgemm_f32_async")
+
+
+def gemm_multi_async(mats: list, x_ptr: int, y_ptrs: list, m: int, flags: int = 0,
+                     stream: int = 0) -> None:
+    """y_i = x * W_i^T for matrices sharing x, in one fused launch
+    (pai_qgemm_f32_multi_async; device pointers)."""
+    n = len(mats)
+    hs = (C.c_void_p * n)(*[w.handle for w in mats])
+    ys = (C.c_void_p * n)(*y_ptrs)
+    check(lib().pai_qgemm_f32_multi_async(hs, n, m, x_ptr, ys, flags | FLAG_DEVICE_PTRS,
+                                          stream or None), "pai_qgemm_f32_multi_async")

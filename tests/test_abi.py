@@ -69,6 +69,12 @@ def test_argument_errors_before_device():
     assert lib.pai_qgemm_f32_async(None, 1, x.ctypes.data, x.ctypes.data, 0, None) == -1
     assert lib.pai_qdequant_f32(None, x.ctypes.data, 0) == -1
     assert lib.pai_qmat_free(None) == 0
+    hs = (C.c_void_p * 1)(None)
+    ys = (C.c_void_p * 1)(x.ctypes.data)
+    assert lib.pai_qgemm_f32_multi_async(None, 1, 1, x.ctypes.data, ys, 1, None) == -1
+    assert lib.pai_qgemm_f32_multi_async(hs, 1, 1, x.ctypes.data, ys, 1, None) == -1
+    assert lib.pai_qgemm_f32_multi_async(hs, 0, 1, x.ctypes.data, ys, 1, None) == -1
+    assert lib.pai_qgemm_f32_multi_async(hs, 5, 1, x.ctypes.data, ys, 1, None) == -1
     assert lib.pai_qmat_bytes(None) == 0
     assert b"NULL" in lib.pai_hip_last_error() or lib.pai_hip_last_error() != b""
 

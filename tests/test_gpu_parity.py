@@ -251,3 +251,76 @@ def test_gpu_argument_errors():
     assert lib.pai_qmat_shape(w.handle, C.byref(t), C.byref(nn), C.byref(kk)) == 0
     assert (t.value, nn.value, kk.value) == (2, 8, 64)
     assert w.nbytes == 8 * 36
+
+
+# ------------------------------------------------------------------ fused projections
+@pytest.mark.parametrize("qtype", [2, 12, 14])
+@pytest.mark.parametrize("m", [1, 3, 40])
+def test_multi_matches_separate_calls(qtype, m):
+    """q/k/v-shaped matrices in one fused call give the same bits as three
+    separate calls (and the oracle's values within the f32 bar)."""
+    from prosperoai_amd.hipmem import DeviceBuffer, Stream
+    k = 1024
+    shapes = [512, 128, 128]
+    say(f"[gpu] multi type={qtype} m={m}")
+    mats, blocks = [], []
+    for i, n in enumerate(shapes):
+        b = weights(qtype, n, k, 900 + 10 * i + qtype)
+        blocks.append(b)
+        mats.append(pa.QMat(qtype, n, k, b))
+    x = pa.normal_f32(77 + m, m * k).reshape(m, k)
+    xd = DeviceBuffer.from_array(x)
+    yd = [DeviceBuffer(m * n * 4) for n in shapes]
+    st = Stream()
+    pa.gemm_multi_async(mats, xd.ptr, [y.ptr for y in yd], m, 0, st.handle)
+    st.synchronize()
+    for w, b, y, n in zip(mats, blocks, yd, shapes):
+        got = y.download((m, n))
+        single = w.gemm(x)
+        assert np.array_equal(got, single)
+        if m < pa.MFMA_MIN_M:
+            assert rel_l2(got, ob.qgemm_seq(qtype, n, k, b, x)) <= TOL_F32
+    st.destroy()
+
+
+def test_multi_rejects_mixed_k():
+    from prosperoai_amd.hipmem import DeviceBuffer
+    say("[gpu] multi mismatch")
+    a = pa.QMat(12, 64, 512, weights(12, 64, 512, 1))
+    b = pa.QMat(12, 64, 256, weights(12, 64, 256, 2))
+    xd, y0, y1 = DeviceBuffer(512 * 4), DeviceBuffer(64 * 4), DeviceBuffer(64 * 4)
+    with pytest.raises(pa.PaiError) as e:
+        pa.gemm_multi_async([a, b], xd.ptr, [y0.ptr, y1.ptr], 1)
+    assert e.value.status == -6
+
+
+def test_graph_replays_match_eager():
+    """GEMV and fused GEMV launches captured into a HIP graph give the eager
+    result on every replay, with eager work between replays."""
+    from prosperoai_amd.hipmem import DeviceBuffer, Graph, Stream
+    say("[gpu] graph replays")
+    k = 2048
+    a = pa.QMat(12, 300, k, weights(12, 300, k, 41))
+    b = pa.QMat(12, 100, k, weights(12, 100, k, 42))
+    x = pa.normal_f32(43, k)
+    xd = DeviceBuffer.from_array(x)
+    ya, yb, yc = DeviceBuffer(300 * 4), DeviceBuffer(100 * 4), DeviceBuffer(300 * 4)
+    st = Stream()
+    want_a, want_b = a.gemm(x.reshape(1, k))[0], b.gemm(x.reshape(1, k))[0]
+
+    def enqueue(sh):
+        pa.gemm_multi_async([a, b], xd.ptr, [ya.ptr, yb.ptr], 1, 0, sh)
+        a.gemm_async(xd.ptr, yc.ptr, 1, 0, sh)
+
+    g = Graph(st, enqueue)
+    for rep in range(4):
+        for buf, n in ((ya, 300), (yb, 100), (yc, 300)):
+            buf.upload(np.full(n, np.nan, np.float32))
+        g.launch(st)
+        st.synchronize()
+        assert np.array_equal(ya.download(300), want_a), rep
+        assert np.array_equal(yb.download(100), want_b), rep
+        assert np.array_equal(yc.download(300), want_a), rep
+        a.gemm(x.reshape(1, k))  # eager work between replays
+    g.destroy()
+    st.destroy()
