@@ -81,11 +81,13 @@ SEPARATE_STEP = [(name, [i]) for i, (name, _, _) in enumerate(PROJ)]
 
 
 def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, plan):
-    """Time `steps` passes over the seven projections, rotating layers. Each
-    layer copy's pass (the launches of `plan`) is captured once into a HIP
-    graph; a step is one graph replay on one stream. The timed region is
-    bracketed by events on that stream, so the GPU time per step is the
-    kernels' time plus the gaps between them inside the graph."""
+    """Time `steps` passes over the seven projections, rotating layers. The
+    passes over all layer copies, in order, are captured once into one HIP
+    graph (as a model's decode step over its layers would be), so a step is
+    the launches of `plan` on one layer copy and there is no host work
+    between steps. The timed region
+    is bracketed by events on the launch stream, so the GPU time per step is
+    the kernels' time plus the gaps between them inside the graph."""
     stream = hm.Stream()
     kmax = max(k for _, _, k in PROJ)
     x = hm.DeviceBuffer.from_array(pa.normal_f32(0xC0DE0000 ^ 0x5A5A, m * kmax))
@@ -99,21 +101,27 @@ def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, plan):
             else:
                 pa.gemm_multi_async([layer.w[i] for i in idx], xp, [yp[i] for i in idx], m, 0, sh)
 
-    graphs = [hm.Graph(stream, lambda sh, l=l: enqueue(l, sh)) for l in layers]
-    for s in range(warmup):
-        graphs[s % len(graphs)].launch(stream)
+    nl = len(layers)
+    graph = hm.Graph(stream, lambda sh: [enqueue(l, sh) for l in layers])
+    rem = steps % nl  # a shorter graph over the first layers finishes the count
+    tail = hm.Graph(stream, lambda sh: [enqueue(l, sh) for l in layers[:rem]]) if rem else None
+    for _ in range(max(1, -(-warmup // nl))):
+        graph.launch(stream)
     stream.synchronize()
     a, b = hm.Event(), hm.Event()
     t0 = time.perf_counter()
     a.record(stream)
-    for s in range(steps):
-        graphs[s % len(graphs)].launch(stream)
+    for _ in range(steps // nl):
+        graph.launch(stream)
+    if tail is not None:
+        tail.launch(stream)
     b.record(stream)
     stream.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = a.elapsed_ms(b)
-    for g in graphs:
-        g.destroy()
+    graph.destroy()
+    if tail is not None:
+        tail.destroy()
     a.destroy(); b.destroy()
     for buf in [x, *ys]:
         buf.free()
@@ -210,6 +218,32 @@ def q8_config1(pa, hm, steps: int) -> dict:
             "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
 
 
+def host_pointer_step(pa, reps: int = 50) -> dict:
+    """The seven Q4_0 projections through the synchronous host-pointer
+    entry point (pai_qgemm_f32 without PAI_QGEMM_DEVICE_PTRS: x is copied
+    to the device and y back over PCIe on every call), wall clock per
+    step. Reported beside the HBM-resident figure, never as the value."""
+    blocks = quantized_layer(pa, pa.Q4_0, 2)
+    layer = Layer(pa, pa.Q4_0, blocks)
+    kmax = max(k for _, _, k in PROJ)
+    x = pa.normal_f32(0xC0DE0000 ^ 0x5A5A, kmax)
+    xs = [x[:k] for _, _, k in PROJ]
+    for w, xv in zip(layer.w, xs):
+        w.gemm(xv)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for w, xv in zip(layer.w, xs):
+            w.gemm(xv)
+        times.append(time.perf_counter() - t0)
+    for w in layer.w:
+        w.free()
+    med = float(np.median(times))
+    b = sum(call_bytes(pa, pa.Q4_0, n, k) for _, n, k in PROJ)
+    return {"us_per_step": round(med * 1e6, 1), "GBps": round(b / med / 1e9, 1),
+            "calls_per_step": len(PROJ)}
+
+
 def prefill(pa, hm, reps: int) -> dict:
     out = {}
     m = 512
@@ -270,6 +304,53 @@ def cpu_baseline(pa, budget_s: float) -> dict:
             "host_cpu": _cpu_model(), "host_nproc": os.cpu_count()}
 
 
+def copy_calibration(hm, mib: int, reps: int = 4) -> None:
+    """`reps` device-to-device copies of `mib` MiB (the runtime's copy
+    kernel): a dispatch whose HBM traffic is known exactly (reads and
+    writes mib MiB each), against which the FETCH_SIZE / WRITE_SIZE counters
+    of a profiling run are scaled."""
+    n = mib << 20
+    src, dst = hm.DeviceBuffer(n), hm.DeviceBuffer(n)
+    st = hm.Stream()
+    for _ in range(reps):
+        hm.hip_check(hm.hip().hipMemcpyAsync(dst.ptr, src.ptr, n, hm.D2D, st.handle),
+                     "hipMemcpyAsync D2D")
+    st.synchronize()
+    st.destroy(); src.free(); dst.free()
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, copy_mib: int, kernel: str) -> dict:
+    """Per-dispatch HBM traffic of `kernel` (a substring of the kernel
+    name) from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB per
+    dispatch), each scaled by the ratio of known bytes to counted bytes of
+    the copy dispatches (copy_calibration) in the same run."""
+    import csv
+
+    def read(path, counter):
+        per = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            key = r["Dispatch_Id"]
+            per.setdefault(key, [r["Kernel_Name"], 0.0])[1] += float(r["Counter_Value"])
+        copies = [v for n, v in per.values() if "copyBuffer" in n]
+        kern = [v for n, v in per.values() if kernel in n]
+        if not copies or not kern:
+            raise RuntimeError(f"{path}: {len(copies)} copy and {len(kern)} '{kernel}' dispatches")
+        copy_bytes = float(copy_mib << 20)
+        scale = copy_bytes / (np.mean(copies) * 1024.0)
+        return np.mean(kern) * 1024.0, scale, len(kern), len(copies), float(np.mean(copies))
+
+    f_b, f_s, nk, nc, f_c = read(fetch_csv, "FETCH_SIZE")
+    w_b, w_s, _, _, w_c = read(write_csv, "WRITE_SIZE")
+    return {"kernel": kernel, "dispatches": nk, "copy_dispatches": nc, "copy_MiB": copy_mib,
+            "copy_fetch_KiB": round(f_c, 1), "copy_write_KiB": round(w_c, 1),
+            "fetch_scale": round(f_s, 4), "write_scale": round(w_s, 4),
+            "fetch_bytes_per_dispatch": round(f_b * f_s),
+            "write_bytes_per_dispatch": round(w_b * w_s),
+            "traffic_bytes_per_launch": round(f_b * f_s + w_b * w_s)}
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -289,7 +370,18 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-launch-detail", action="store_true",
+                    help="skip the per-launch timings of the headline step")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="end with device copies of this size (counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "this script with --calib-copy-mib, then exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.calib_copy_mib or 64,
+                                     "k_gemv<paik::Q4_0")))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(the path has no multi-GPU sharding in this build)", file=sys.stderr)
@@ -300,9 +392,10 @@ def main() -> int:
     pa.init()
     log(f"Q4_0 M=1 x {args.layers} layers")
 
-    head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup)
+    head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup,
+                       launch_detail=not args.no_launch_detail)
     log(f"Q4_0 M=1 fused step: {head['GBps']:.1f} GB/s wall, {head['gpu_GBps']:.1f} GB/s GPU; "
-        f"{head['per_launch']}")
+        f"{head.get('per_launch')}")
     avg_us = head["gpu_ms_per_step"] * 1e3 / head["launches_per_step"]
     roof = {"bound": "hbm", "achieved": round(head["gpu_GBps"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(head["gpu_GBps"] / HBM_PEAK_GBS, 4),
@@ -310,9 +403,11 @@ def main() -> int:
             "launches_per_step": head["launches_per_step"],
             "bytes_per_launch": round(head["bytes_per_step"] / head["launches_per_step"]),
             "avg_launch_us": round(avg_us, 3)}
-    traffic_file = ROOT / "profiles" / "traffic_gemv_q4_0.json"
-    if traffic_file.exists():
-        roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+    traffic_file = ROOT / "profiles" / "traffic_gemv_q4_0_decode_step.txt"
+    if traffic_file.exists():  # measured by two counter runs of this script (see the file)
+        for ln in traffic_file.read_text().splitlines():
+            if ln.startswith("traffic_bytes_per_launch:"):
+                roof["traffic"] = int(ln.split(":", 1)[1])
 
     extra = {}
     if not args.no_extra:
@@ -327,10 +422,14 @@ def main() -> int:
                 extra[f"q4_k_m{m}"] = gemv_config(pa, hm, pa.Q4_K, 3, m, args.layers, 100, 5)
                 log(f"Q4_K M={m}: {extra[f'q4_k_m{m}']['gpu_GBps']:.1f} GB/s GPU")
             extra["q8_0_4096x4096_m1"] = q8_config1(pa, hm, 300)
+            extra["q4_0_m1_host_pointers"] = host_pointer_step(pa)
+            log(f"Q4_0 M=1 host pointers: {extra['q4_0_m1_host_pointers']}")
             extra["prefill_m512"] = prefill(pa, hm, 20)
             log(f"prefill: {extra['prefill_m512']}")
         except Exception as e:  # extras never hide the headline
             extra["error"] = repr(e)
+    if args.calib_copy_mib:
+        copy_calibration(hm, args.calib_copy_mib)
     cpu = None
     if not args.no_cpu:
         try:

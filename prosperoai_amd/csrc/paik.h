@@ -3,22 +3,26 @@
  * kernels (*.hip). Plain C so both sides include it.
  *
  * Device layout of a packed matrix W[N][K] ("planes", one allocation).
- * The bytes are the native GGUF block bytes, regrouped so that each lane
- * of a wavefront can fetch its 32-element "chunk" of a row with one
- * 16-byte load of codes plus a small scale fetch:
+ * The native GGUF block bytes are regrouped by "chunk" (32 consecutive
+ * columns of a row) so that one lane of a wavefront fetches a chunk's
+ * codes with one 16-byte load (two for Q8_0) plus its block's scales.
+ * Codes are stored as the nibble words described in qdev.h (word j holds
+ * columns 8j..8j+7; byte m = column 8j+m low, 8j+m+4 high), as signed
+ * 4-bit fields where the format allows:
  *
- *   Q8_0: q  = int8 codes      [N][K]      (block b at bytes 32b..32b+31)
- *         d  = f16 scales      [N][K/32]
- *   Q4_0: q  = nibble bytes    [N][K/2]    (block b at bytes 16b..16b+15)
- *         d  = f16 scales      [N][K/32]
- *   Q4_K: q  = nibble bytes    [N][K/2]    (super-block b at 128b, native)
- *         meta = 16-byte heads [N][K/256]  (f16 d, f16 dmin, 12 scale bytes)
- *   Q6_K: q  = ql bytes        [N][K/2]    (super-block b at 128b; within
- *              each 64-byte half, 16-byte chunk t holds ql[8t..8t+7] then
- *              ql[32+8t..32+8t+7])
- *         aux = qh bytes       [N][K/4]    (native)
- *         meta = int8 scales   [N][K/256][16] (native)
- *         d  = f16 scales      [N][K/256]
+ *   Q8_0: q    [N][K]       chunk c at 32c: 16 B of low nibbles (l - 8),
+ *                           then 16 B of signed high nibbles h
+ *         d    [N][K/32]    f16 block scales
+ *   Q4_0: q    [N][K/2]     chunk c at 16c: codes n - 8
+ *         d    [N][K/32]    f16 block scales
+ *   Q4_K: q    [N][K/2]     chunk c (sub-block c%8 of super-block c/8) at
+ *                           16c: codes n - 8
+ *         meta [N][K/256]   16-byte heads, native (f16 d, f16 dmin, 12
+ *                           bytes of packed 6-bit scales and mins)
+ *   Q6_K: q    [N][K/2]     chunk c at 16c: low 4 code bits minus 8
+ *         aux  [N][K/4]     chunk c at 8c: the 2 high code bits, two words
+ *         meta [N][K/256][16] int8 sub-block scales, native
+ *         d    [N][K/256]   f16 super-block scales
  *
  * Total bytes equal N * type_bytes(K): the re-layout moves bytes, it does
  * not add any.

@@ -3,7 +3,8 @@
 Mirrors the reference's operator contract: the C entry points return
 pai_status_t and never allocate the caller's buffers; here a non-zero status
 raises PaiError carrying the status name and the library's message.
-torch tensors (device memory, streams) are plumbing only; every kernel runs
+Device buffers, streams and graphs for the device-pointer entry points come
+from hipmem (the HIP runtime libpai_hip.so links); every kernel runs
 through libpai_hip.so.
 """
 from __future__ import annotations
@@ -106,7 +107,7 @@ class QMat:
         check(lib().pai_qdequant_f32(self._h, out.ctypes.data, 0), "pai_qdequant_f32")
         return out
 
-    # ---- device-pointer entry points (torch tensors as plumbing) ----
+    # ---- device-pointer entry points (raw device addresses, hipStream_t) ----
     def gemm_async(self, x_ptr: int, y_ptr: int, m: int, flags: int = 0, stream: int = 0) -> None:
         check(lib().pai_qgemm_f32_async(self._h, m, x_ptr, y_ptr, flags | FLAG_DEVICE_PTRS,
                                         stream or None), "pai_qgemm_f32_async")
