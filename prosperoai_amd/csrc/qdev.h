@@ -270,14 +270,12 @@ struct Q4_0 {
  * endian words). adapters/llama/gguf.c:639-648. */
 __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
                                              uint32_t &sc, uint32_t &mn) {
-  if (j < 4u) {
-    sc = byte_of(s0, (int)j) & 63u;
-    mn = byte_of(s1, (int)j) & 63u;
-  } else {
-    const int i = (int)j - 4;
-    sc = (byte_of(s2, i) & 0x0Fu) | ((byte_of(s0, i) >> 6) << 4);
-    mn = (byte_of(s2, i) >> 4) | ((byte_of(s1, i) >> 6) << 4);
-  }
+  /* both cases computed and selected (j differs between lanes) */
+  const int i = (int)(j & 3u);
+  const uint32_t b0 = byte_of(s0, i), b1 = byte_of(s1, i), b2 = byte_of(s2, i);
+  const bool lo = j < 4u;
+  sc = lo ? (b0 & 63u) : ((b2 & 0x0Fu) | ((b0 >> 6) << 4));
+  mn = lo ? (b1 & 63u) : ((b2 >> 4) | ((b1 >> 6) << 4));
 }
 
 /* adapters/llama/gguf.c:852-882. Chunk c is sub-block j = c % 8 of
@@ -303,6 +301,22 @@ struct Q4_K {
     w.q = bl16(r.q, 16u * lane, row * r.q_stride + 16u * cb);
     w.m = bl16(r.meta, 16u * (lane >> 3), (row * r.nb + (cb >> 3)) * 16u);
     return w;
+  }
+  /* the same for sub-block j = 4 HI + i, with HI known at compile time */
+  template <int HI>
+  __device__ static void scales_half(const Raw &w, uint32_t i, float &d1, float &m1) {
+    const uint32_t b0 = byte_of(w.m.y, (int)i), b1 = byte_of(w.m.z, (int)i);
+    uint32_t s, mn;
+    if constexpr (HI) {
+      const uint32_t b2 = byte_of(w.m.w, (int)i);
+      s = (b2 & 0x0Fu) | ((b0 >> 6) << 4);
+      mn = (b2 >> 4) | ((b1 >> 6) << 4);
+    } else {
+      s = b0 & 63u;
+      mn = b1 & 63u;
+    }
+    d1 = h2f_lo(w.m.x) * (float)s;
+    m1 = h2f_hi(w.m.x) * (float)mn;
   }
   __device__ static void scales(const Raw &w, uint32_t c, float &d1, float &m1) {
     uint32_t s, mn;

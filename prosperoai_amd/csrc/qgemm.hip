@@ -1,194 +1,523 @@
 /*
  * Batched / prefill GEMM over packed blocks on MFMA (gfx950).
  *
- * y[M][N] = x[M][K] · Wᵀ with W dequantized tile by tile into LDS as fp16
- * (or bf16), x converted to the same type, v_mfma_f32_16x16x32_{f16,bf16}
- * with f32 accumulation.
+ * y[M][N] = x[M][K] · Wᵀ: weights dequantized in registers to fp16 (or
+ * bf16), activations rounded to the same type through LDS,
+ * v_mfma_f32_16x16x32_{f16,bf16} with f32 accumulation.
  *
- * Workgroup tile: 128 weight rows x 128 tokens; K advances 64 columns (two
- * 32-column chunks) per step. 256 threads: in a step every thread fetches
- * one chunk of one weight row and dequantizes it exactly (the reference's
- * f32 values, then one rounding to 16 bits), and converts eight float4 of
- * activations (a load instruction covers four tokens' 256 contiguous
- * bytes); both land in the step's LDS buffer. The loads of step s+1 are issued before the MFMAs of
- * step s, and the two LDS buffers alternate, so the fetch, the dequant and
- * the matrix work of neighbouring steps overlap.
+ * Workgroup: 4 waves, 256 weight rows x TT tokens (TT = 128 or 32); each
+ * wave owns 64 rows (four 16-row groups) and all TT tokens, so no weight
+ * value is shared between waves and the weights never pass through LDS:
+ * a lane fetches whole chunks straight into registers and turns them into
+ * MFMA operands. A step covers 128 columns, i.e. four chunks per row.
  *
- * Four waves in a 2x2 grid each own a 64x64 output block: per 32-column
- * slice a wave reads four 16-row A fragments and four 16-token B fragments
- * from LDS and issues 16 MFMAs.
+ * Operand layout of v_mfma_f32_16x16x32_*: lane l supplies row l%16 of A
+ * and column l%16 of B, each with 8 K values ("k-set" l/16); D[4(l/16)+i]
+ * [l%16] lands in lane l. Because every operand is already scaled, the
+ * four k-sets of one MFMA need not come from the same chunk: lane (r, g)
+ * (r = l%16, g = l/16) loads chunk 4s+g of row r, and MFMA number w of the
+ * step (w = 0..3) takes nibble word w of that chunk (its columns
+ * 8w..8w+7) as the k-set. The B lane (t, g) reads the matching 8
+ * activations x[t][128s + 32g + 8w ..] from LDS. One 16-byte load per lane
+ * thus covers 4 chunks of 16 rows (64 contiguous bytes of each row).
  *
- * Operand layout used for v_mfma_f32_16x16x32_*: lane l supplies row
- * (l % 16) of the A tile and column (l % 16) of the B tile, each with the
- * 8 K values [8*(l/16), 8*(l/16)+8) of the 32-wide slice; both operands
- * use the same K assignment, so the product is the full 32-term dot
- * product. Lane l receives D[4*(l/16) + i][l % 16], i = 0..3.
+ * Dequantization to 16 bits costs about two VALU operations per weight:
+ * the 4-bit (or 6- and 8-bit) codes are gathered into bytes, v_perm_b32
+ * turns byte pairs into the fp16 values 1024 + q, and v_fma_mix computes
+ * (1024 + q) * s + b in f32 precision with one rounding to fp16, where
+ * s, b fold the block scale, the code offset and (Q4_K) the block minimum:
+ * value = s * q' + b equals the reference's f32 value to within one f32
+ * rounding of b, far below the fp16 rounding that follows.
+ *
+ * Per step a wave issues 4 x (TT/16) x 4 MFMAs; the dequantization of the
+ * next step's operands (loaded a full step earlier) and the conversion of
+ * the next activation tile into the other LDS buffer are interleaved with
+ * them. Shapes with few tiles split K across workgroups whose partial sums
+ * are added into y (zeroed first) with f32 atomics.
+ *
+ * Workgroups are numbered so that the ones resident on one XCD (hardware
+ * places workgroup i on XCD i % 8) take consecutive tiles of one token
+ * tile: their activations are shared through that XCD's L2.
  */
+#include <type_traits>
+
 #include "qdev.h"
 
 namespace paik {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16x_t __attribute__((ext_vector_type(16)));
 
-constexpr int BN = 128, BM = 128, BK = 64;
-constexpr int LDK = BK + 8; /* LDS row pitch in 16-bit elements (bank spread) */
-
-template <bool BF>
-__device__ __forceinline__ uint16_t to16(float f) {
-  if constexpr (BF) return __builtin_bit_cast(uint16_t, (__bf16)f);
-  else return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
+constexpr int kGW = 4;               /* waves per workgroup */
+constexpr int kRowsWG = 64 * kGW;    /* weight rows per workgroup */
+constexpr int kKStep = 128;          /* columns per step */
+constexpr int kXPitch = kKStep + 8;  /* LDS row pitch of the activation tile (16-bit units) */
+constexpr int kXcds = 8;
+constexpr int kTPitch = 68; /* floats per token row of the output transpose (64 + pad) */
 
 template <bool BF>
-__device__ __forceinline__ f4_t mfma(const uint4 &a, const uint4 &b, f4_t c) {
+__device__ __forceinline__ f16x_t mfma(const uint4 &a, const uint4 &b, f16x_t c) {
   if constexpr (BF)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8_t, a),
                                                    __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, a),
                                                   __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
-  return (uint32_t)lo | ((uint32_t)hi << 16);
+/* Two bytes of `bytes` (selector picks them) as the fp16 values 1024 + b. */
+__device__ __forceinline__ uint32_t magic2(uint32_t bytes, uint32_t sel) {
+  return __builtin_amdgcn_perm(0x64646464u, bytes, sel);
 }
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 
-/* 32 values -> 16-bit, stored as four 16-byte words at dst */
+/* (1024 + q) * s + b for the two fp16 halves of m, as two 16-bit results
+ * (fp16: the compiler emits v_fma_mixlo/hi_f16, f32 arithmetic with one
+ * rounding to fp16; bf16: f32 FMA then a packed round-to-nearest-even
+ * conversion). Written in plain C++ rather than asm so that the compiler
+ * sees every register write (MFMA source hazards). */
 template <bool BF>
-__device__ __forceinline__ void put32(uint16_t *dst, const float o[32]) {
-#pragma unroll
-  for (int i = 0; i < 32; i += 8) {
-    uint4 p;
-    p.x = pack2(to16<BF>(o[i]), to16<BF>(o[i + 1]));
-    p.y = pack2(to16<BF>(o[i + 2]), to16<BF>(o[i + 3]));
-    p.z = pack2(to16<BF>(o[i + 4]), to16<BF>(o[i + 5]));
-    p.w = pack2(to16<BF>(o[i + 6]), to16<BF>(o[i + 7]));
-    *reinterpret_cast<uint4 *>(dst + i) = p;
+__device__ __forceinline__ uint32_t scale2(uint32_t m, float s, float b) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t h = __builtin_bit_cast(h2_t, m);
+  const float lo = __builtin_fmaf((float)h[0], s, b), hi = __builtin_fmaf((float)h[1], s, b);
+  if constexpr (BF) {
+    typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+    const b2_t p = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, p);
+  } else {
+    const h2_t p = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, p);
   }
 }
 
-/* What one thread fetches for one K step: one weight chunk (row tid/2,
- * chunk tid%2) and eight float4 of activations (token tid/16 + 16i,
- * columns 4*(tid%16)..+3), so that the 64 lanes of a load instruction read
- * four tokens' 256 contiguous bytes each. */
-template <class F>
-struct StepRegs {
-  typename F::Raw w;
-  float4 xv[8];
-  bool wv;
+/* Operand of one nibble word: lo holds columns 0..3 (byte m = column m),
+ * hi columns 4..7, as unsigned byte codes q; value = s * (1024 + q) + b. */
+template <bool BF>
+__device__ __forceinline__ uint4 word_op(uint32_t lo, uint32_t hi, float s, float b) {
+  uint4 o;
+  o.x = scale2<BF>(magic2(lo, kSel01), s, b);
+  o.y = scale2<BF>(magic2(lo, kSel23), s, b);
+  o.z = scale2<BF>(magic2(hi, kSel01), s, b);
+  o.w = scale2<BF>(magic2(hi, kSel23), s, b);
+  return o;
+}
+
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  return (a & mask) | (b & ~mask);
+}
+
+/* Operands of a chunk, per format: scale<P>(w, c, ok) computes the f32
+ * factors once per chunk (`ok` false gives zeros, for a chunk past the end
+ * of the row; P = c / 4 % 2, the parity of the step, which fixes the half
+ * of a Q4_K super-block the chunk lies in); word(w, j, sc) returns the
+ * operand of nibble word j. */
+template <class F, bool BF>
+struct Ops;
+
+template <bool BF>
+struct Ops<Q4_0, BF> {
+  struct Sc { float s, b; };
+  template <int P>
+  __device__ static Sc scale(const Q4_0::Raw &w, uint32_t, bool ok) {
+    const float d = ok ? h2f(w.d) : 0.0f;
+    return {d, -1032.0f * d}; /* d (n - 8), n = q */
+  }
+  __device__ static uint4 word(const Q4_0::Raw &w, int j, const Sc &sc) {
+    const uint32_t u = word4(w.q, j) ^ 0x88888888u; /* stored n - 8 -> n */
+    return word_op<BF>(u & 0x0F0F0F0Fu, (u >> 4) & 0x0F0F0F0Fu, sc.s, sc.b);
+  }
 };
 
-template <class F, bool BF>
-__global__ void __launch_bounds__(256) k_gemm(paik_qview_t v, const float *__restrict__ x,
-                                              float *__restrict__ y, uint32_t m) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][BM * LDK];
+template <bool BF>
+struct Ops<Q4_K, BF> {
+  struct Sc { float s, b; };
+  template <int P>
+  __device__ static Sc scale(const Q4_K::Raw &w, uint32_t c, bool ok) {
+    float d1, m1;
+    Q4_K::scales_half<P>(w, c & 3u, d1, m1);
+    if (!ok) d1 = m1 = 0.0f;
+    return {d1, -fmaf(1024.0f, d1, m1)}; /* d1 n - m1 */
+  }
+  __device__ static uint4 word(const Q4_K::Raw &w, int j, const Sc &sc) {
+    const uint32_t u = word4(w.q, j) ^ 0x88888888u;
+    return word_op<BF>(u & 0x0F0F0F0Fu, (u >> 4) & 0x0F0F0F0Fu, sc.s, sc.b);
+  }
+};
 
-  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
-  const uint32_t n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+template <bool BF>
+struct Ops<Q8_0, BF> {
+  struct Sc { float s, b; };
+  template <int P>
+  __device__ static Sc scale(const Q8_0::Raw &w, uint32_t, bool ok) {
+    const float d = ok ? h2f(w.d) : 0.0f;
+    return {d, -1152.0f * d};
+  }
+  /* byte = l | (h + 8) << 4 = code + 128 */
+  __device__ static uint4 word(const Q8_0::Raw &w, int j, const Sc &sc) {
+    const uint32_t l = word4(w.lo, j) ^ 0x88888888u, h = word4(w.hi, j) ^ 0x88888888u;
+    return word_op<BF>(bfi(0xF0F0F0F0u, h << 4, l), bfi(0xF0F0F0F0u, h, l >> 4), sc.s, sc.b);
+  }
+};
+
+template <bool BF>
+struct Ops<Q6_K, BF> {
+  struct Sc { float s0, b0, s1, b1; }; /* columns 0..15, 16..31 */
+  template <int P>
+  __device__ static Sc scale(const Q6_K::Raw &w, uint32_t, bool ok) {
+    const float d = ok ? h2f(w.d) : 0.0f;
+    const float s0 = d * Q6_K::scale(w, 0), s1 = d * Q6_K::scale(w, 1);
+    return {s0, -1056.0f * s0, s1, -1056.0f * s1}; /* d sc (q - 32) */
+  }
+  /* byte = l | h2 << 4 = q (0..63) */
+  __device__ static uint4 word(const Q6_K::Raw &w, int j, const Sc &sc) {
+    const uint32_t e = j < 2 ? w.qh.x : w.qh.y;
+    const uint32_t h = ((j & 1) ? (e >> 2) : e) & 0x33333333u;
+    const uint32_t l = word4(w.ql, j) ^ 0x88888888u;
+    return word_op<BF>(bfi(0xF0F0F0F0u, h << 4, l), bfi(0xF0F0F0F0u, h, l >> 4),
+                       j < 2 ? sc.s0 : sc.s1, j < 2 ? sc.b0 : sc.b1);
+  }
+};
+
+__device__ __forceinline__ uint32_t cvt2(float a, float b, bool bf) {
+  if (bf) {
+    typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+    const b2_t p = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  const h2_t p = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+/* Chunk c of a row through the plane buffer resources, with per-lane row
+ * and chunk (every lane of the GEMM has its own row). */
+template <class F>
+struct GLoad;
+template <>
+struct GLoad<Q4_0> {
+  __device__ static Q4_0::Raw get(const QRes &r, uint32_t row, uint32_t c) {
+    Q4_0::Raw w;
+    w.q = bl16(r.q, row * r.q_stride + 16u * c, 0);
+    w.d = bl2(r.d, (row * r.nb + c) * 2u, 0);
+    return w;
+  }
+};
+template <>
+struct GLoad<Q8_0> {
+  __device__ static Q8_0::Raw get(const QRes &r, uint32_t row, uint32_t c) {
+    Q8_0::Raw w;
+    const uint32_t o = row * r.q_stride + 32u * c;
+    w.lo = bl16(r.q, o, 0);
+    w.hi = bl16(r.q, o + 16u, 0);
+    w.d = bl2(r.d, (row * r.nb + c) * 2u, 0);
+    return w;
+  }
+};
+template <>
+struct GLoad<Q4_K> {
+  __device__ static Q4_K::Raw get(const QRes &r, uint32_t row, uint32_t c) {
+    Q4_K::Raw w;
+    w.q = bl16(r.q, row * r.q_stride + 16u * c, 0);
+    w.m = bl16(r.meta, (row * r.nb + (c >> 3)) * 16u, 0);
+    return w;
+  }
+};
+template <>
+struct GLoad<Q6_K> {
+  __device__ static Q6_K::Raw get(const QRes &r, uint32_t row, uint32_t c) {
+    const uint32_t blk = row * r.nb + (c >> 3);
+    Q6_K::Raw w;
+    w.ql = bl16(r.q, row * r.q_stride + 16u * c, 0);
+    w.qh = bl8(r.aux, row * r.k4 + 8u * c, 0);
+    w.sc = bl2(r.meta, blk * 16u + 2u * (c & 7u), 0);
+    w.d = bl2(r.d, blk * 2u, 0);
+    return w;
+  }
+};
+
+struct GemmArgs {
+  paik_qview_t v;
+  const float *x;
+  float *y;
+  uint32_t m;
+  uint32_t tiles_n, tiles_m, splits; /* grid: tiles_n * tiles_m * splits (padded to kXcds) */
+  uint32_t per_xcd;                  /* workgroups per XCD */
+  uint32_t x_bytes;                  /* m * k * 4 (< 2^31) */
+  uint32_t steps_per_split;
+  int vec_store; /* y rows 16-byte aligned and n % 4 == 0 */
+};
+
+template <class F, bool BF, int TT>
+__global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
+  constexpr int JT = TT / 32; /* 32-token fragments */
+  /* activation double buffer; after the main loop, the output transpose
+   * (4 waves x 32 tokens x kTPitch floats) */
+  constexpr int kXsHalves = 2 * TT * kXPitch > 2 * 4 * 32 * kTPitch ? TT * kXPitch : 4 * 32 * kTPitch;
+  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][kXsHalves];
+
+  const paik_qview_t &v = a.v;
+  /* tile of this workgroup: XCD-major numbering (see the top of the file) */
+  const uint32_t logical = (blockIdx.x % kXcds) * a.per_xcd + blockIdx.x / kXcds;
+  const uint32_t ntile = a.tiles_n * a.tiles_m;
+  if (logical >= ntile * a.splits) return;
+  const uint32_t split = logical / ntile, tile = logical % ntile;
+  const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
+  const uint32_t n0 = tn * (uint32_t)kRowsWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
-  const uint32_t nsteps = (nchunks + 1u) >> 1;
+  const uint32_t nsteps = (nchunks + 3u) >> 2;
+  const uint32_t s0 = split * a.steps_per_split; /* < nsteps */
+  const uint32_t s1 = s0 + a.steps_per_split;     /* multiple of 4, may pass nsteps */
 
-  /* this thread's share of a step */
-  const int rr = tid >> 1, hf = tid & 1; /* weight row, chunk half */
-  const int xt = tid >> 4, x4 = tid & 15; /* first token, float4 column */
-  const uint32_t wrow = n0 + (uint32_t)rr;
+  const int tid = (int)threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, g = lane >> 5;
+  static_assert(sizeof(Xs) >= 4u * 32u * kTPitch * sizeof(float), "transpose fits");
 
-  auto fetch = [&](uint32_t s, StepRegs<F> &r) {
-    const uint32_t c = 2u * s + (uint32_t)hf;
-    r.wv = wrow < v.n && c < nchunks;
-    if (r.wv) r.w = F::load(v, wrow, c);
-    const uint32_t col = 64u * s + 4u * (uint32_t)x4;
+  /* this lane's weight rows (one per 32-row fragment), clamped for loads */
+  uint32_t rows[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t tok = m0 + (uint32_t)(xt + 16 * i);
-      r.xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (tok < m && col < v.k)
-        r.xv[i] = *reinterpret_cast<const float4 *>(x + (size_t)tok * v.k + col);
+  for (int i = 0; i < 2; ++i)
+    rows[i] = min(n0 + (uint32_t)(64 * wave + 32 * i + r), v.n - 1u);
+
+  const QRes res = make_qres(v);
+  typedef typename F::Raw Raw;
+  /* chunk 4s + 2u + g of each of the lane's rows, u = 0, 1 */
+  auto load_w = [&](uint32_t s, Raw (&dst)[4]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        dst[2 * i + u] = GLoad<F>::get(res, rows[i], min(4u * s + 2u * u + (uint32_t)g, nchunks - 1u));
+  };
+  /* x tile of a step: thread (tid/8, tid%8) loads, for each token quarter
+   * tq and column quarter cq, the float4 at token tid/8 + 32 tq, columns
+   * 32 cq + 4 (tid%8) .. +3 of the step: 8 lanes read one token's 128
+   * contiguous bytes. Tokens past m read as zero (offset beyond the buffer
+   * resource), and so do columns past k. */
+  constexpr int TQ = TT / 32;
+  constexpr int XH = 2 * TQ; /* float4 per thread in half a tile */
+  const __amdgpu_buffer_rsrc_t xres = plane_rsrc(a.x, a.x_bytes);
+  const uint32_t xtok = (uint32_t)tid >> 3, xcw = 4u * ((uint32_t)tid & 7u);
+  uint32_t xoff[TQ];
+#pragma unroll
+  for (int tq = 0; tq < TQ; ++tq) {
+    const uint32_t tok = m0 + xtok + 32u * (uint32_t)tq;
+    xoff[tq] = tok < a.m ? (tok * v.k + xcw) * 4u : 0x80000000u;
+  }
+  /* the tile is moved in two halves (items tq * 4 + cq below and at or
+   * above 2 TQ), so that only half of it is held in registers */
+  auto load_x = [&](uint32_t s, int h, float4 (&xr)[XH]) {
+#pragma unroll
+    for (int e = 0; e < XH; ++e) {
+      const int f = h * XH + e, tq = f >> 2, cq = f & 3;
+      /* a column quarter past k reads as zero too (uniform select, no
+       * branch: the loads of a step stay one straight run) */
+      const bool cok = kKStep * s + 32u * (uint32_t)cq < v.k;
+      const uint32_t off = cok ? xoff[tq] + 128u * (uint32_t)cq : 0x80000000u;
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(xres, (int)off, (int)(512u * s), 0);
+      /* element access by index: a bit cast of an ext-vector member (q.y)
+       * is compiled as a cast of the vector's first element */
+      xr[e] = make_float4(__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]),
+                          __uint_as_float(q[3]));
     }
   };
-  auto stage = [&](uint32_t s, const StepRegs<F> &r, int buf) {
-    const uint32_t c = 2u * s + (uint32_t)hf;
-    float o[32];
-    if (r.wv) {
-      F::dequant(r.w, c, o);
-    } else {
+  auto store_x = [&](int buf, int h, const float4 (&xr)[XH]) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) o[i] = 0.0f;
-    }
-    put32<BF>(&Ws[buf][rr * LDK + 32 * hf], o);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 f = r.xv[i];
+    for (int e = 0; e < XH; ++e) {
+      const int f = h * XH + e, tq = f >> 2, cq = f & 3;
       uint2 p;
-      p.x = pack2(to16<BF>(f.x), to16<BF>(f.y));
-      p.y = pack2(to16<BF>(f.z), to16<BF>(f.w));
-      *reinterpret_cast<uint2 *>(&Xs[buf][(xt + 16 * i) * LDK + 4 * x4]) = p;
+      p.x = cvt2(xr[e].x, xr[e].y, BF);
+      p.y = cvt2(xr[e].z, xr[e].w, BF);
+      *reinterpret_cast<uint2 *>(
+          &Xs[buf][(xtok + 32u * (uint32_t)tq) * kXPitch + 32u * (uint32_t)cq + xcw]) = p;
     }
   };
 
-  f4_t acc[4][4];
+  using Op = Ops<F, BF>;
+  f16x_t acc[2][JT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < JT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  StepRegs<F> r;
-  fetch(0u, r);
-  stage(0u, r, 0);
-  __syncthreads();
-
-  for (uint32_t s = 0; s < nsteps; ++s) {
-    const int cur = (int)(s & 1u);
-    const bool more = s + 1u < nsteps;
-    if (more) fetch(s + 1u, r); /* in flight during this step's MFMAs */
+  /* Step s: the raw chunks of step s (wc, requested two steps earlier)
+   * are turned into operands just before their MFMAs, and those of step
+   * s+2 are requested into wn; the activations of step s+1 (two register
+   * halves, each requested a step earlier) move into the other LDS buffer,
+   * each half followed by the request of the same half of step s+2. */
+  float4 xr0[XH], xr1[XH];
+  auto step = [&](auto kk, uint32_t s, const Raw (&wc)[4], Raw (&wn)[4]) {
+    constexpr int P = decltype(kk)::value & 1; /* s % 2 (s0 % 4 == 0) */
+    constexpr int cur = P;
+    load_w(s + 2u, wn);
+    typename Op::Sc sc[4];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      const int ko = kk + 8 * (lane >> 4);
-      uint4 a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const uint4 *>(
-            &Ws[cur][(wr * 64 + i * 16 + (lane & 15)) * LDK + ko]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const uint4 *>(
-            &Xs[cur][(wc * 64 + j * 16 + (lane & 15)) * LDK + ko]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<BF>(a[i], b[j], acc[i][j]);
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t c = 4u * s + 2u * (uint32_t)(q & 1) + (uint32_t)g;
+      sc[q] = Op::template scale<P>(wc[q], c, c < nchunks);
     }
-    if (more) stage(s + 1u, r, cur ^ 1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint4 A[2], b[JT];
+#pragma unroll
+        for (int j = 0; j < JT; ++j)
+          b[j] = *reinterpret_cast<const uint4 *>(
+              &Xs[cur][(32 * j + r) * kXPitch + 32 * (2 * u + g) + 8 * w]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) A[i] = Op::word(wc[2 * i + u], w, sc[2 * i + u]);
+#pragma unroll
+        for (int j = 0; j < JT; ++j)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) acc[i][j] = mfma<BF>(A[i], b[j], acc[i][j]);
+      }
+      if (u == 0) {
+        store_x(cur ^ 1, 0, xr0);
+        load_x(s + 2u, 0, xr0);
+      }
+    }
+    store_x(cur ^ 1, 1, xr1);
+    load_x(s + 2u, 1, xr1);
     __syncthreads();
+  };
+
+  /* The step range [s0, s1) has a length divisible by 4; steps at or past
+   * the end of the row have zero operands (scale 0, activations read as
+   * 0). The loads issued in the last steps are not used. */
+  Raw w0[4], w1[4], w2[4], w3[4];
+  load_w(s0, w0);
+  load_w(s0 + 1u, w1);
+  load_x(s0, 0, xr0);
+  load_x(s0, 1, xr1);
+  store_x(0, 0, xr0);
+  store_x(0, 1, xr1);
+  load_x(s0 + 1u, 0, xr0);
+  load_x(s0 + 1u, 1, xr1);
+  __syncthreads();
+  /* four steps per iteration: the four raw-chunk buffers rotate without
+   * register copies, and the body has no branch, so each load is waited
+   * for only where its data is used */
+  for (uint32_t s = s0; s < s1; s += 4u) {
+    step(std::integral_constant<int, 0>(), s, w0, w2);
+    step(std::integral_constant<int, 1>(), s + 1u, w1, w3);
+    step(std::integral_constant<int, 2>(), s + 2u, w2, w0);
+    step(std::integral_constant<int, 3>(), s + 3u, w3, w1);
   }
 
-  /* D[row][tok]: rows 4*(lane/16)+q, token lane%16 of each 16x16 tile */
+  /* D of v_mfma_f32_32x32x16: lane (r, g) holds rows 8 (e/4) + 4 g + e % 4
+   * of the 32-row fragment, token r of the 32-token fragment. Each
+   * 32-token fragment is transposed through LDS (the activation buffers
+   * are free after the last barrier), so that a lane then owns one row and
+   * every store or atomic add of a wave covers 64 consecutive outputs of
+   * one token. */
+  const bool split_k = a.splits > 1u;
+  float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTPitch);
+  const uint32_t orow = n0 + (uint32_t)(64 * wave + lane);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int j = 0; j < JT; ++j) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t tok = m0 + (uint32_t)(wc * 64 + j * 16 + (lane & 15));
-      const uint32_t rb = n0 + (uint32_t)(wr * 64 + i * 16 + 4 * (lane >> 4));
-      if (tok >= m) continue;
-      float *dst = y + (size_t)tok * v.n;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        if (rb + (uint32_t)q < v.n) dst[rb + (uint32_t)q] = acc[i][j][q];
+        *reinterpret_cast<float4 *>(&Ts[r * kTPitch + 32 * i + 8 * q + 4 * g]) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]);
+#pragma unroll 4
+    for (int t = 0; t < 32; ++t) {
+      const float val = Ts[t * kTPitch + lane];
+      const uint32_t tok = m0 + (uint32_t)(32 * j + t);
+      if (tok < a.m && orow < v.n) {
+        float *dst = a.y + (size_t)tok * v.n + orow;
+        if (split_k) unsafeAtomicAdd(dst, val);
+        else *dst = val;
+      }
     }
   }
+}
+
+/* y[0 .. count) = 0 (a kernel, so that the call can be captured into a
+ * graph). */
+__global__ void __launch_bounds__(256) k_zero(float4 *__restrict__ y, size_t n4, float *tail,
+                                              uint32_t ntail) {
+  const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+  if (i < n4) y[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i < ntail) tail[i] = 0.0f;
+}
+
+static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
+  const size_t head = ((16u - ((uintptr_t)y & 15u)) & 15u) / 4u; /* floats before 16-B alignment */
+  const size_t pre = head < count ? head : count;
+  const size_t n4 = (count - pre) / 4u, rest = count - pre - 4u * n4;
+  /* the unaligned head and the tail: at most 6 floats, done by one thread each */
+  if (pre) k_zero<<<1, 256, 0, s>>>(nullptr, 0, y, (uint32_t)pre);
+  if (rest) k_zero<<<1, 256, 0, s>>>(nullptr, 0, y + pre + 4u * n4, (uint32_t)rest);
+  if (n4) {
+    const size_t blocks = (n4 + 255u) / 256u;
+    k_zero<<<dim3((unsigned)blocks), 256, 0, s>>>(reinterpret_cast<float4 *>(y + pre), n4,
+                                                   nullptr, 0);
+  }
+  return hipGetLastError();
+}
+
+template <class F, int TT>
+static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y, bool bf16,
+                            hipStream_t s) {
+  GemmArgs a;
+  a.v = v;
+  a.x = x;
+  a.y = y;
+  a.m = m;
+  a.tiles_n = (v.n + kRowsWG - 1u) / kRowsWG;
+  a.tiles_m = (m + TT - 1u) / TT;
+  const uint32_t tiles = a.tiles_n * a.tiles_m;
+  const uint32_t nsteps = ((v.k >> 5) + 3u) >> 2;
+  /* split K while the grid would leave most CUs idle (256 CUs), keeping
+   * at least 8 steps per split */
+  uint32_t splits = 1;
+  while (tiles * splits * 2u <= 256u && nsteps / (splits * 2u) >= 8u) splits *= 2u;
+  if (const char *e = getenv("PAI_GEMM_SPLITS")) {
+    const int r = atoi(e);
+    if (r >= 1 && r <= 64) splits = (uint32_t)r;
+  }
+  a.steps_per_split = (nsteps + splits - 1u) / splits;
+  a.steps_per_split = (a.steps_per_split + 3u) & ~3u; /* the loop runs steps in fours */
+  a.splits = (nsteps + a.steps_per_split - 1u) / a.steps_per_split;
+  const uint32_t total = tiles * a.splits;
+  a.per_xcd = (total + kXcds - 1u) / kXcds;
+  a.vec_store = (v.n % 4u == 0u && ((uintptr_t)y & 15u) == 0u) ? 1 : 0;
+  a.x_bytes = (uint32_t)((size_t)m * v.k * 4u);
+  if (a.splits > 1u) {
+    const hipError_t e = zero_fill(y, (size_t)m * v.n, s);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid(a.per_xcd * kXcds), block(64 * kGW);
+  if (bf16) k_gemm<F, true, TT><<<grid, block, 0, s>>>(a);
+  else k_gemm<F, false, TT><<<grid, block, 0, s>>>(a);
+  return hipGetLastError();
 }
 
 template <class F>
 static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x, float *y,
                               bool bf16, hipStream_t s) {
-  const dim3 grid((v.n + BN - 1) / BN, (m + BM - 1) / BM), block(256);
-  if (bf16) k_gemm<F, true><<<grid, block, 0, s>>>(v, x, y, m);
-  else k_gemm<F, false><<<grid, block, 0, s>>>(v, x, y, m);
-  return hipGetLastError();
+  /* token blocks whose activations span less than 2^31 bytes (32-bit
+   * buffer offsets) */
+  const size_t row_bytes = (size_t)v.k * 4u;
+  uint32_t blk = (uint32_t)((0x7FFFFFFFu / row_bytes) & ~127u);
+  if (blk == 0u) return hipErrorInvalidValue; /* k > 4M columns */
+  for (uint32_t t0 = 0; t0 < m; t0 += blk) {
+    const uint32_t mt = m - t0 < blk ? m - t0 : blk;
+    const float *xt = x + (size_t)t0 * v.k;
+    float *yt = y + (size_t)t0 * v.n;
+    const hipError_t e = mt <= 32u ? launch_tt<F, 32>(v, mt, xt, yt, bf16, s)
+                                   : launch_tt<F, 128>(v, mt, xt, yt, bf16, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 } // namespace paik

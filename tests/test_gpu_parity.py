@@ -209,6 +209,31 @@ def test_prefill_shape_gate_q4k_m512():
     assert rel_l2(y[rows], ref) <= TOL_F16
 
 
+def test_prefill_shape_down_q6k_m512():
+    """Few output tiles: the K range is split across workgroups."""
+    qtype, (n, k), m = 14, LLAMA8B["down"], 512
+    say("[gpu] prefill down Q6_K M=512 (split K)")
+    blocks = weights(qtype, n, k, 0xC0DE0046)
+    x = pa.normal_f32(0xC0DE0046 ^ 0x5A5A, m * k).reshape(m, k)
+    y = pa.QMat(qtype, n, k, blocks).gemm(x)
+    rows = np.arange(3, m, 41)
+    ref = ob.qgemm_f64(qtype, n, k, blocks, x[rows])
+    assert rel_l2(y[rows], ref) <= TOL_F16
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7])
+def test_mfma_forced_split_k_ragged(monkeypatch, splits):
+    """K split into uneven ranges, last step with a single chunk."""
+    monkeypatch.setenv("PAI_GEMM_SPLITS", str(splits))
+    for qtype, m in ((2, 70), (8, 33)):
+        n, k = 300, 32 * 37
+        say(f"[gpu] gemm MFMA split={splits} type={qtype} m={m}")
+        blocks = weights(qtype, n, k, 90 + splits + qtype)
+        x = pa.normal_f32(91 + splits, m * k).reshape(m, k)
+        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        assert rel_l2(y, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
+
+
 # ------------------------------------------------------------------ device pointers
 def test_device_pointer_path_matches_host_path():
     from prosperoai_amd.hipmem import DeviceBuffer, Stream
