@@ -49,12 +49,14 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
 typedef float f16x_t __attribute__((ext_vector_type(16)));
 
-constexpr int kGW = 4;               /* waves per workgroup */
-constexpr int kRowsWG = 64 * kGW;    /* weight rows per workgroup */
+#ifndef PAI_GEMM_WAVES
+#define PAI_GEMM_WAVES 8
+#endif
+constexpr int kGemmWaves = PAI_GEMM_WAVES; /* waves per workgroup (4: 64 rows each, 8: 32) */
+constexpr int kRowsWG = 256;               /* weight rows per workgroup */
 constexpr int kKStep = 128;          /* columns per step */
 constexpr int kXPitch = kKStep + 8;  /* LDS row pitch of the activation tile (16-bit units) */
 constexpr int kXcds = 8;
-constexpr int kTPitch = 68; /* floats per token row of the output transpose (64 + pad) */
 
 template <bool BF>
 __device__ __forceinline__ f16x_t mfma(const uint4 &a, const uint4 &b, f16x_t c) {
@@ -246,15 +248,22 @@ struct GemmArgs {
   uint32_t per_xcd;                  /* workgroups per XCD */
   uint32_t x_bytes;                  /* m * k * 4 (< 2^31) */
   uint32_t steps_per_split;
-  int vec_store; /* y rows 16-byte aligned and n % 4 == 0 */
 };
 
-template <class F, bool BF, int TT>
-__global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
-  constexpr int JT = TT / 32; /* 32-token fragments */
+template <class F, bool BF, int TT, int NW>
+__global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
+  constexpr int NT = 64 * NW;             /* threads */
+  constexpr int RF = kRowsWG / (32 * NW); /* 32-row fragments per wave */
+  constexpr int RW = 32 * RF;             /* rows per wave */
+  constexpr int JT = TT / 32;             /* 32-token fragments */
+  constexpr int XI = TT * 32 / NT;        /* float4 of activations per thread per step */
+  constexpr int XH = XI / 2;              /* ... per half step */
+  static_assert(RF >= 1 && XH >= 1, "tile shape");
   /* activation double buffer; after the main loop, the output transpose
-   * (4 waves x 32 tokens x kTPitch floats) */
-  constexpr int kXsHalves = 2 * TT * kXPitch > 2 * 4 * 32 * kTPitch ? TT * kXPitch : 4 * 32 * kTPitch;
+   * (NW waves x 32 tokens x (RW + 4) floats) */
+  constexpr int kTP = RW + 4;
+  constexpr int kTBytes = NW * 32 * kTP * 4;
+  constexpr int kXsHalves = 4 * TT * kXPitch >= kTBytes ? TT * kXPitch : kTBytes / 4;
   __shared__ __attribute__((aligned(16))) uint16_t Xs[2][kXsHalves];
 
   const paik_qview_t &v = a.v;
@@ -266,56 +275,48 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
   const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
   const uint32_t n0 = tn * (uint32_t)kRowsWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
-  const uint32_t nsteps = (nchunks + 3u) >> 2;
-  const uint32_t s0 = split * a.steps_per_split; /* < nsteps */
-  const uint32_t s1 = s0 + a.steps_per_split;     /* multiple of 4, may pass nsteps */
+  const uint32_t s0 = split * a.steps_per_split; /* < number of steps */
+  const uint32_t s1 = s0 + a.steps_per_split;     /* multiple of 4, may pass the row end */
 
   const int tid = (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, g = lane >> 5;
-  static_assert(sizeof(Xs) >= 4u * 32u * kTPitch * sizeof(float), "transpose fits");
 
   /* this lane's weight rows (one per 32-row fragment), clamped for loads */
-  uint32_t rows[2];
+  uint32_t rows[RF];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    rows[i] = min(n0 + (uint32_t)(64 * wave + 32 * i + r), v.n - 1u);
+  for (int i = 0; i < RF; ++i)
+    rows[i] = min(n0 + (uint32_t)(RW * wave + 32 * i + r), v.n - 1u);
 
   const QRes res = make_qres(v);
   typedef typename F::Raw Raw;
   /* chunk 4s + 2u + g of each of the lane's rows, u = 0, 1 */
-  auto load_w = [&](uint32_t s, Raw (&dst)[4]) {
+  auto load_w = [&](uint32_t s, Raw (&dst)[2 * RF]) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RF; ++i)
 #pragma unroll
       for (int u = 0; u < 2; ++u)
         dst[2 * i + u] = GLoad<F>::get(res, rows[i], min(4u * s + 2u * u + (uint32_t)g, nchunks - 1u));
   };
-  /* x tile of a step: thread (tid/8, tid%8) loads, for each token quarter
-   * tq and column quarter cq, the float4 at token tid/8 + 32 tq, columns
-   * 32 cq + 4 (tid%8) .. +3 of the step: 8 lanes read one token's 128
-   * contiguous bytes. Tokens past m read as zero (offset beyond the buffer
-   * resource), and so do columns past k. */
-  constexpr int TQ = TT / 32;
-  constexpr int XH = 2 * TQ; /* float4 per thread in half a tile */
+  /* Activation tile of a step (TT tokens x 128 columns): item tid + NT e
+   * is the float4 at token item / 32, columns 4 (item % 32) .. +3, so 32
+   * lanes read one token's 512 contiguous bytes. Tokens past m and
+   * columns past k read as zero (offsets beyond the buffer resource). The
+   * tile moves in two halves (items e < XH and e >= XH) so that only half
+   * of it is held in registers at a time. */
   const __amdgpu_buffer_rsrc_t xres = plane_rsrc(a.x, a.x_bytes);
-  const uint32_t xtok = (uint32_t)tid >> 3, xcw = 4u * ((uint32_t)tid & 7u);
-  uint32_t xoff[TQ];
+  const uint32_t xcol = 4u * ((uint32_t)tid & 31u), xt = (uint32_t)tid >> 5;
+  uint32_t xoff[XI];
 #pragma unroll
-  for (int tq = 0; tq < TQ; ++tq) {
-    const uint32_t tok = m0 + xtok + 32u * (uint32_t)tq;
-    xoff[tq] = tok < a.m ? (tok * v.k + xcw) * 4u : 0x80000000u;
+  for (int e = 0; e < XI; ++e) {
+    const uint32_t tok = m0 + xt + (uint32_t)(NT / 32) * (uint32_t)e;
+    xoff[e] = tok < a.m ? (tok * v.k + xcol) * 4u : 0x80000000u;
   }
-  /* the tile is moved in two halves (items tq * 4 + cq below and at or
-   * above 2 TQ), so that only half of it is held in registers */
   auto load_x = [&](uint32_t s, int h, float4 (&xr)[XH]) {
+    const bool cok = kKStep * s + xcol < v.k;
 #pragma unroll
     for (int e = 0; e < XH; ++e) {
-      const int f = h * XH + e, tq = f >> 2, cq = f & 3;
-      /* a column quarter past k reads as zero too (uniform select, no
-       * branch: the loads of a step stay one straight run) */
-      const bool cok = kKStep * s + 32u * (uint32_t)cq < v.k;
-      const uint32_t off = cok ? xoff[tq] + 128u * (uint32_t)cq : 0x80000000u;
+      const uint32_t off = cok ? xoff[h * XH + e] : 0x80000000u;
       const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(xres, (int)off, (int)(512u * s), 0);
       /* element access by index: a bit cast of an ext-vector member (q.y)
        * is compiled as a cast of the vector's first element */
@@ -326,19 +327,18 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
   auto store_x = [&](int buf, int h, const float4 (&xr)[XH]) {
 #pragma unroll
     for (int e = 0; e < XH; ++e) {
-      const int f = h * XH + e, tq = f >> 2, cq = f & 3;
+      const uint32_t t = xt + (uint32_t)(NT / 32) * (uint32_t)(h * XH + e);
       uint2 p;
       p.x = cvt2(xr[e].x, xr[e].y, BF);
       p.y = cvt2(xr[e].z, xr[e].w, BF);
-      *reinterpret_cast<uint2 *>(
-          &Xs[buf][(xtok + 32u * (uint32_t)tq) * kXPitch + 32u * (uint32_t)cq + xcw]) = p;
+      *reinterpret_cast<uint2 *>(&Xs[buf][t * kXPitch + xcol]) = p;
     }
   };
 
   using Op = Ops<F, BF>;
-  f16x_t acc[2][JT];
+  f16x_t acc[RF][JT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RF; ++i)
 #pragma unroll
     for (int j = 0; j < JT; ++j)
 #pragma unroll
@@ -350,13 +350,13 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
    * halves, each requested a step earlier) move into the other LDS buffer,
    * each half followed by the request of the same half of step s+2. */
   float4 xr0[XH], xr1[XH];
-  auto step = [&](auto kk, uint32_t s, const Raw (&wc)[4], Raw (&wn)[4]) {
+  auto step = [&](auto kk, uint32_t s, const Raw (&wc)[2 * RF], Raw (&wn)[2 * RF]) {
     constexpr int P = decltype(kk)::value & 1; /* s % 2 (s0 % 4 == 0) */
     constexpr int cur = P;
     load_w(s + 2u, wn);
-    typename Op::Sc sc[4];
+    typename Op::Sc sc[2 * RF];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2 * RF; ++q) {
       const uint32_t c = 4u * s + 2u * (uint32_t)(q & 1) + (uint32_t)g;
       sc[q] = Op::template scale<P>(wc[q], c, c < nchunks);
     }
@@ -364,17 +364,17 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        uint4 A[2], b[JT];
+        uint4 A[RF], b[JT];
 #pragma unroll
         for (int j = 0; j < JT; ++j)
           b[j] = *reinterpret_cast<const uint4 *>(
               &Xs[cur][(32 * j + r) * kXPitch + 32 * (2 * u + g) + 8 * w]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) A[i] = Op::word(wc[2 * i + u], w, sc[2 * i + u]);
+        for (int i = 0; i < RF; ++i) A[i] = Op::word(wc[2 * i + u], w, sc[2 * i + u]);
 #pragma unroll
         for (int j = 0; j < JT; ++j)
 #pragma unroll
-          for (int i = 0; i < 2; ++i) acc[i][j] = mfma<BF>(A[i], b[j], acc[i][j]);
+          for (int i = 0; i < RF; ++i) acc[i][j] = mfma<BF>(A[i], b[j], acc[i][j]);
       }
       if (u == 0) {
         store_x(cur ^ 1, 0, xr0);
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
   /* The step range [s0, s1) has a length divisible by 4; steps at or past
    * the end of the row have zero operands (scale 0, activations read as
    * 0). The loads issued in the last steps are not used. */
-  Raw w0[4], w1[4], w2[4], w3[4];
+  Raw w0[2 * RF], w1[2 * RF], w2[2 * RF], w3[2 * RF];
   load_w(s0, w0);
   load_w(s0 + 1u, w1);
   load_x(s0, 0, xr0);
@@ -413,24 +413,26 @@ __global__ void __launch_bounds__(64 * kGW, 1) k_gemm(GemmArgs a) {
    * of the 32-row fragment, token r of the 32-token fragment. Each
    * 32-token fragment is transposed through LDS (the activation buffers
    * are free after the last barrier), so that a lane then owns one row and
-   * every store or atomic add of a wave covers 64 consecutive outputs of
+   * every store or atomic add of a wave covers RW consecutive outputs of
    * one token. */
   const bool split_k = a.splits > 1u;
-  float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTPitch);
-  const uint32_t orow = n0 + (uint32_t)(64 * wave + lane);
+  float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTP);
+  constexpr int TPI = 64 / RW; /* tokens per read-out instruction */
+  const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
 #pragma unroll
   for (int j = 0; j < JT; ++j) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < RF; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4 *>(&Ts[r * kTPitch + 32 * i + 8 * q + 4 * g]) =
+        *reinterpret_cast<float4 *>(&Ts[r * kTP + 32 * i + 8 * q + 4 * g]) =
             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                         acc[i][j][4 * q + 3]);
 #pragma unroll 4
-    for (int t = 0; t < 32; ++t) {
-      const float val = Ts[t * kTPitch + lane];
-      const uint32_t tok = m0 + (uint32_t)(32 * j + t);
+    for (int t = 0; t < 32; t += TPI) {
+      const int tt = t + lane / RW;
+      const float val = Ts[tt * kTP + lane % RW];
+      const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         float *dst = a.y + (size_t)tok * v.n + orow;
         if (split_k) unsafeAtomicAdd(dst, val);
@@ -464,7 +466,7 @@ static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <class F, int TT>
+template <class F, int TT, int NW>
 static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y, bool bf16,
                             hipStream_t s) {
   GemmArgs a;
@@ -489,15 +491,14 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
   a.splits = (nsteps + a.steps_per_split - 1u) / a.steps_per_split;
   const uint32_t total = tiles * a.splits;
   a.per_xcd = (total + kXcds - 1u) / kXcds;
-  a.vec_store = (v.n % 4u == 0u && ((uintptr_t)y & 15u) == 0u) ? 1 : 0;
   a.x_bytes = (uint32_t)((size_t)m * v.k * 4u);
   if (a.splits > 1u) {
     const hipError_t e = zero_fill(y, (size_t)m * v.n, s);
     if (e != hipSuccess) return e;
   }
-  const dim3 grid(a.per_xcd * kXcds), block(64 * kGW);
-  if (bf16) k_gemm<F, true, TT><<<grid, block, 0, s>>>(a);
-  else k_gemm<F, false, TT><<<grid, block, 0, s>>>(a);
+  const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
+  if (bf16) k_gemm<F, true, TT, NW><<<grid, block, 0, s>>>(a);
+  else k_gemm<F, false, TT, NW><<<grid, block, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -513,8 +514,8 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
     const uint32_t mt = m - t0 < blk ? m - t0 : blk;
     const float *xt = x + (size_t)t0 * v.k;
     float *yt = y + (size_t)t0 * v.n;
-    const hipError_t e = mt <= 32u ? launch_tt<F, 32>(v, mt, xt, yt, bf16, s)
-                                   : launch_tt<F, 128>(v, mt, xt, yt, bf16, s);
+    const hipError_t e = mt <= 32u ? launch_tt<F, 32, kGemmWaves>(v, mt, xt, yt, bf16, s)
+                                   : launch_tt<F, 128, kGemmWaves>(v, mt, xt, yt, bf16, s);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
