@@ -26,6 +26,10 @@ struct pai_qmat {
   uint64_t dev_bytes;
   int device;
   paik_qview_t view;
+  /* 16-bit copy of the activations for the MFMA path (see x16_workspace);
+   * guarded by g_x16_lock */
+  void *x16;
+  uint64_t x16_bytes;
 };
 
 /* ---------------------------------------------------------------------- */
@@ -299,6 +303,7 @@ pai_status_t pai_qmat_upload_device(pai_qmat_t **out, uint32_t type, uint64_t n,
 
 pai_status_t pai_qmat_free(pai_qmat_t *w) {
   if (w == NULL) return PAI_OK;
+  if (w->x16 != NULL) (void)hipFree(w->x16);
   hipError_t e = hipFree(w->dev);
   free(w);
   return e == hipSuccess ? PAI_OK : map_hip(e, "hipFree(weights)");
@@ -320,13 +325,55 @@ uint64_t pai_qmat_bytes(const pai_qmat_t *w) { return w != NULL ? w->packed_byte
 
 #define PAI_MFMA_MIN_M 32u
 
+/* Workspace of the MFMA path: a 16-bit copy of up to PAI_X16_TOKENS tokens
+ * of activations, owned by the matrix handle (calls on one handle do not
+ * overlap, so they can share it). Allocated, or grown, by the first call
+ * that needs it outside stream capture; a call made during capture uses
+ * what is there (larger inputs run in token blocks of that size) or, with
+ * nothing there, the kernels that stage the activations through registers.
+ * Both give the same results. */
+#define PAI_X16_TOKENS 1024u
+static pthread_mutex_t g_x16_lock = PTHREAD_MUTEX_INITIALIZER;
+
+static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint64_t *bytes) {
+  pai_qmat_t *w = (pai_qmat_t *)cw;
+  const uint64_t tok = ((m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS) + 255u) & ~(uint64_t)255u;
+  const uint64_t want = tok * w->k * 2u;
+  pthread_mutex_lock(&g_x16_lock);
+  if (w->x16 == NULL || w->x16_bytes < want) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+      void *p = NULL;
+      if (w->x16 != NULL) {
+        (void)hipStreamSynchronize(s); /* earlier calls on s may still read it */
+        (void)hipFree(w->x16);
+        w->x16 = NULL;
+        w->x16_bytes = 0;
+      }
+      if (hipMalloc(&p, want) == hipSuccess) {
+        w->x16 = p;
+        w->x16_bytes = want;
+      } else {
+        (void)hipGetLastError(); /* no workspace: the register-staged kernels run */
+      }
+    }
+  }
+  void *p = w->x16;
+  *bytes = w->x16_bytes;
+  pthread_mutex_unlock(&g_x16_lock);
+  return p;
+}
+
 static pai_status_t launch(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
                            uint32_t flags, hipStream_t s) {
   int e;
   if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
     e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
   } else {
-    e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, (flags & PAI_QGEMM_MFMA_BF16) != 0u, s);
+    uint64_t wb = 0;
+    void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(w, m, s, &wb);
+    e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb,
+                       s);
   }
   return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
 }

@@ -64,8 +64,11 @@ int paik_gemv(const paik_qview_t *v, uint32_t m, const float *x, float *y,
  * count, in one launch per group of up to 4 tokens. */
 int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys,
                     uint32_t count, uint32_t m, const float *x, void *stream);
+/* x16 (may be NULL): device workspace of x16_bytes for a 16-bit copy of
+ * the activations; with it the activations move into LDS by DMA. */
 int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
-                   float *y, int bf16, void *stream);
+                   float *y, int bf16, void *x16, uint64_t x16_bytes,
+                   void *stream);
 
 #ifdef __cplusplus
 }

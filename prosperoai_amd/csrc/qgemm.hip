@@ -39,6 +39,8 @@
  * places workgroup i on XCD i % 8) take consecutive tiles of one token
  * tile: their activations are shared through that XCD's L2.
  */
+#include <string.h>
+
 #include <type_traits>
 
 #include "qdev.h"
@@ -49,11 +51,6 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
 typedef float f16x_t __attribute__((ext_vector_type(16)));
 
-#ifndef PAI_GEMM_WAVES
-#define PAI_GEMM_WAVES 8
-#endif
-constexpr int kGemmWaves = PAI_GEMM_WAVES; /* waves per workgroup (4: 64 rows each, 8: 32) */
-constexpr int kRowsWG = 256;               /* weight rows per workgroup */
 constexpr int kKStep = 128;          /* columns per step */
 constexpr int kXPitch = kKStep + 8;  /* LDS row pitch of the activation tile (16-bit units) */
 constexpr int kXcds = 8;
@@ -199,6 +196,7 @@ template <class F>
 struct GLoad;
 template <>
 struct GLoad<Q4_0> {
+  static constexpr int kLoads = 2; /* vector memory instructions per chunk */
   __device__ static Q4_0::Raw get(const QRes &r, uint32_t row, uint32_t c) {
     Q4_0::Raw w;
     w.q = bl16(r.q, row * r.q_stride + 16u * c, 0);
@@ -208,6 +206,7 @@ struct GLoad<Q4_0> {
 };
 template <>
 struct GLoad<Q8_0> {
+  static constexpr int kLoads = 3;
   __device__ static Q8_0::Raw get(const QRes &r, uint32_t row, uint32_t c) {
     Q8_0::Raw w;
     const uint32_t o = row * r.q_stride + 32u * c;
@@ -219,6 +218,7 @@ struct GLoad<Q8_0> {
 };
 template <>
 struct GLoad<Q4_K> {
+  static constexpr int kLoads = 2;
   __device__ static Q4_K::Raw get(const QRes &r, uint32_t row, uint32_t c) {
     Q4_K::Raw w;
     w.q = bl16(r.q, row * r.q_stride + 16u * c, 0);
@@ -228,6 +228,7 @@ struct GLoad<Q4_K> {
 };
 template <>
 struct GLoad<Q6_K> {
+  static constexpr int kLoads = 4;
   __device__ static Q6_K::Raw get(const QRes &r, uint32_t row, uint32_t c) {
     const uint32_t blk = row * r.nb + (c >> 3);
     Q6_K::Raw w;
@@ -242,6 +243,7 @@ struct GLoad<Q6_K> {
 struct GemmArgs {
   paik_qview_t v;
   const float *x;
+  const uint16_t *x16; /* activations already rounded to 16 bits (k_gemm_x16) */
   float *y;
   uint32_t m;
   uint32_t tiles_n, tiles_m, splits; /* grid: tiles_n * tiles_m * splits (padded to kXcds) */
@@ -250,10 +252,14 @@ struct GemmArgs {
   uint32_t steps_per_split;
 };
 
-template <class F, bool BF, int TT, int NW>
+/* Tile shapes: TT tokens x RWG weight rows, NW waves of RWG/NW rows; XB
+ * activation half-tiles held in registers (2: each half requested a full
+ * step ahead; 1: the second half only half a step ahead, for tiles whose
+ * halves are large). */
+template <class F, bool BF, int TT, int NW, int RWG, int XB>
 __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
-  constexpr int NT = 64 * NW;             /* threads */
-  constexpr int RF = kRowsWG / (32 * NW); /* 32-row fragments per wave */
+  constexpr int NT = 64 * NW;         /* threads */
+  constexpr int RF = RWG / (32 * NW); /* 32-row fragments per wave */
   constexpr int RW = 32 * RF;             /* rows per wave */
   constexpr int JT = TT / 32;             /* 32-token fragments */
   constexpr int XI = TT * 32 / NT;        /* float4 of activations per thread per step */
@@ -273,7 +279,7 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
   if (logical >= ntile * a.splits) return;
   const uint32_t split = logical / ntile, tile = logical % ntile;
   const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
-  const uint32_t n0 = tn * (uint32_t)kRowsWG, m0 = tm * (uint32_t)TT;
+  const uint32_t n0 = tn * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
   const uint32_t s0 = split * a.steps_per_split; /* < number of steps */
   const uint32_t s1 = s0 + a.steps_per_split;     /* multiple of 4, may pass the row end */
@@ -349,7 +355,8 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
    * s+2 are requested into wn; the activations of step s+1 (two register
    * halves, each requested a step earlier) move into the other LDS buffer,
    * each half followed by the request of the same half of step s+2. */
-  float4 xr0[XH], xr1[XH];
+  float4 xr0[XH], xr1[XB == 2 ? XH : 1];
+  float4 (&xrh)[XH] = *reinterpret_cast<float4 (*)[XH]>(XB == 2 ? &xr1[0] : &xr0[0]);
   auto step = [&](auto kk, uint32_t s, const Raw (&wc)[2 * RF], Raw (&wn)[2 * RF]) {
     constexpr int P = decltype(kk)::value & 1; /* s % 2 (s0 % 4 == 0) */
     constexpr int cur = P;
@@ -360,29 +367,47 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
       const uint32_t c = 4u * s + 2u * (uint32_t)(q & 1) + (uint32_t)g;
       sc[q] = Op::template scale<P>(wc[q], c, c < nchunks);
     }
+    /* eight sub-steps k = 4u + w (chunk pair u, nibble word w): the
+     * activation operands of sub-step k+1 are read from LDS before the
+     * MFMAs of sub-step k, and its weight operands are dequantized after
+     * them, so both overlap the matrix work */
+    auto opsB = [&](int k, uint4 (&b)[JT]) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+      for (int j = 0; j < JT; ++j)
+        b[j] = *reinterpret_cast<const uint4 *>(
+            &Xs[cur][(32 * j + r) * kXPitch + 32 * (2 * (k >> 2) + g) + 8 * (k & 3)]);
+    };
+    auto opsA = [&](int k, uint4 (&A)[RF]) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        uint4 A[RF], b[JT];
+      for (int i = 0; i < RF; ++i) A[i] = Op::word(wc[2 * i + (k >> 2)], k & 3, sc[2 * i + (k >> 2)]);
+    };
+    uint4 Ac[RF], bc[JT];
+    opsB(0, bc);
+    opsA(0, Ac);
 #pragma unroll
-        for (int j = 0; j < JT; ++j)
-          b[j] = *reinterpret_cast<const uint4 *>(
-              &Xs[cur][(32 * j + r) * kXPitch + 32 * (2 * u + g) + 8 * w]);
+    for (int k = 0; k < 8; ++k) {
+      uint4 An[RF], bn[JT];
+      if (k < 7) opsB(k + 1, bn);
 #pragma unroll
-        for (int i = 0; i < RF; ++i) A[i] = Op::word(wc[2 * i + u], w, sc[2 * i + u]);
+      for (int j = 0; j < JT; ++j)
 #pragma unroll
-        for (int j = 0; j < JT; ++j)
-#pragma unroll
-          for (int i = 0; i < RF; ++i) acc[i][j] = mfma<BF>(A[i], b[j], acc[i][j]);
-      }
-      if (u == 0) {
+        for (int i = 0; i < RF; ++i) acc[i][j] = mfma<BF>(Ac[i], bc[j], acc[i][j]);
+      if (k < 7) opsA(k + 1, An);
+      if (k == 3) {
         store_x(cur ^ 1, 0, xr0);
-        load_x(s + 2u, 0, xr0);
+        if constexpr (XB == 2) load_x(s + 2u, 0, xr0);
+        else load_x(s + 1u, 1, xr0);
+      }
+      if (k < 7) {
+#pragma unroll
+        for (int i = 0; i < RF; ++i) Ac[i] = An[i];
+#pragma unroll
+        for (int j = 0; j < JT; ++j) bc[j] = bn[j];
       }
     }
-    store_x(cur ^ 1, 1, xr1);
-    load_x(s + 2u, 1, xr1);
+    store_x(cur ^ 1, 1, xrh);
+    if constexpr (XB == 2) load_x(s + 2u, 1, xrh);
+    else load_x(s + 2u, 0, xrh);
     __syncthreads();
   };
 
@@ -393,11 +418,11 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
   load_w(s0, w0);
   load_w(s0 + 1u, w1);
   load_x(s0, 0, xr0);
-  load_x(s0, 1, xr1);
   store_x(0, 0, xr0);
-  store_x(0, 1, xr1);
+  load_x(s0, 1, xrh);
+  store_x(0, 1, xrh);
   load_x(s0 + 1u, 0, xr0);
-  load_x(s0 + 1u, 1, xr1);
+  if constexpr (XB == 2) load_x(s0 + 1u, 1, xrh);
   __syncthreads();
   /* four steps per iteration: the four raw-chunk buffers rotate without
    * register copies, and the body has no branch, so each load is waited
@@ -418,6 +443,235 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
   const bool split_k = a.splits > 1u;
   float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW; /* tokens per read-out instruction */
+  const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
+#pragma unroll
+  for (int j = 0; j < JT; ++j) {
+#pragma unroll
+    for (int i = 0; i < RF; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4 *>(&Ts[r * kTP + 32 * i + 8 * q + 4 * g]) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                        acc[i][j][4 * q + 3]);
+#pragma unroll 4
+    for (int t = 0; t < 32; t += TPI) {
+      const int tt = t + lane / RW;
+      const float val = Ts[tt * kTP + lane % RW];
+      const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
+      if (tok < a.m && orow < v.n) {
+        float *dst = a.y + (size_t)tok * v.n + orow;
+        if (split_k) unsafeAtomicAdd(dst, val);
+        else *dst = val;
+      }
+    }
+  }
+}
+
+/* s_waitcnt on the vector memory counter only (gfx9 encoding: vmcnt bits
+ * 3:0 and 15:14; expcnt and lgkmcnt at their maximum, i.e. not waited). */
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+/* x[m][k] f32 -> 16-bit copy (fp16 or bf16, round to nearest even), four
+ * values per thread. */
+__global__ void __launch_bounds__(256) k_cvt_x(const float4 *__restrict__ x,
+                                               uint2 *__restrict__ out, size_t n4, int bf) {
+  const size_t stride = (size_t)gridDim.x * 256u;
+  for (size_t i = (size_t)blockIdx.x * 256u + threadIdx.x; i < n4; i += stride) {
+    const float4 f = x[i];
+    uint2 p;
+    p.x = cvt2(f.x, f.y, bf != 0);
+    p.y = cvt2(f.z, f.w, bf != 0);
+    out[i] = p;
+  }
+}
+
+/* The same GEMM with the activations taken from their 16-bit copy and moved
+ * from memory straight into LDS (buffer_load ... lds), so they use neither
+ * registers nor VALU work. A tile row (token) of a step is 128 columns =
+ * 256 bytes = 16 segments of 16 bytes; segment q of token t sits at position
+ * q ^ (t % 16) of the row, which spreads the operand reads of 16 lanes (16
+ * consecutive tokens, same segment) over all LDS banks. One DMA instruction
+ * fills 4 token rows (1 KiB, lane l: token 4i + l/16, position l % 16). */
+template <class F, bool BF, int TT, int NW, int RWG>
+__global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
+  constexpr int NT = 64 * NW;
+  constexpr int RF = RWG / (32 * NW);
+  constexpr int RW = 32 * RF;
+  constexpr int JT = TT / 32;
+  constexpr int XQ = TT / (4 * NW); /* DMA instructions per wave per step */
+  constexpr int kTileBytes = TT * 256;
+  constexpr int kTP = RW + 4;
+  constexpr int kTBytes = NW * 32 * kTP * 4;
+  constexpr int kLdsBytes = 2 * kTileBytes >= kTBytes ? 2 * kTileBytes : kTBytes;
+  static_assert(RF >= 1 && XQ >= 1 && NT <= 512, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint8_t Xb[kLdsBytes];
+
+  const paik_qview_t &v = a.v;
+  const uint32_t logical = (blockIdx.x % kXcds) * a.per_xcd + blockIdx.x / kXcds;
+  const uint32_t ntile = a.tiles_n * a.tiles_m;
+  if (logical >= ntile * a.splits) return;
+  const uint32_t split = logical / ntile, tile = logical % ntile;
+  const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
+  const uint32_t n0 = tn * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
+  const uint32_t nchunks = v.k >> 5;
+  const uint32_t s0 = split * a.steps_per_split;
+  const uint32_t s1 = s0 + a.steps_per_split;
+
+  const int tid = (int)threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, g = lane >> 5;
+
+  uint32_t rows[RF];
+#pragma unroll
+  for (int i = 0; i < RF; ++i)
+    rows[i] = min(n0 + (uint32_t)(RW * wave + 32 * i + r), v.n - 1u);
+  const QRes res = make_qres(v);
+  typedef typename F::Raw Raw;
+  constexpr int kWLoads = 2 * RF * GLoad<F>::kLoads; /* vector loads issued by load_w */
+  auto load_w = [&](uint32_t s, Raw (&dst)[2 * RF]) {
+#pragma unroll
+    for (int i = 0; i < RF; ++i)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        dst[2 * i + u] = GLoad<F>::get(res, rows[i], min(4u * s + 2u * u + (uint32_t)g, nchunks - 1u));
+  };
+
+  /* this lane's DMA items: instruction q moves token rows 4 (wave + NW q)
+   * .. +3; the lane fills position p = lane % 16 of row t with segment
+   * p ^ (t % 16) */
+  const __amdgpu_buffer_rsrc_t xres = plane_rsrc(a.x16, a.x_bytes);
+  uint32_t doff[XQ], dcol[XQ];
+#pragma unroll
+  for (int q = 0; q < XQ; ++q) {
+    const uint32_t t = 4u * (uint32_t)(wave + NW * q) + ((uint32_t)lane >> 4);
+    const uint32_t seg = ((uint32_t)lane & 15u) ^ (t & 15u);
+    const uint32_t tok = m0 + t;
+    dcol[q] = 8u * seg;
+    doff[q] = tok < a.m ? (tok * v.k + 8u * seg) * 2u : 0x80000000u;
+  }
+  /* Written as asm rather than the buffer-load-to-LDS builtin: the compiler
+   * cannot tell which LDS buffer a DMA writes and would wait for every
+   * outstanding load before each LDS read; here the waits are explicit
+   * (wait_vmem and the barrier at the end of a step). M0 (the LDS base of
+   * the DMA) is saved and restored around the load. */
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)Xb;
+  auto dma_x = [&](uint32_t s, int buf) {
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+      /* columns past k read as zero (offset beyond the resource) */
+      const uint32_t off = kKStep * s + dcol[q] < v.k ? doff[q] : 0x80000000u;
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(
+          (int)(lds0 + (uint32_t)(buf * kTileBytes + 4 * (wave + NW * q) * 256)));
+      const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)(256u * s));
+      uint32_t saved;
+      __asm__ volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %1\n\t"
+          "s_nop 4\n\t"
+          "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "s"(dst), "v"(off), "s"(xres), "s"(soff)
+          : "memory");
+    }
+  };
+
+  using Op = Ops<F, BF>;
+  f16x_t acc[RF][JT];
+#pragma unroll
+  for (int i = 0; i < RF; ++i)
+#pragma unroll
+    for (int j = 0; j < JT; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  /* Step s: the MFMAs run on the chunks of step s (wc) and the activation
+   * tile of step s; after its second sub-step the activations of step s+1
+   * are requested into the other LDS buffer and the raw chunks of step s+2
+   * into wn; at the end, the wait leaves only the chunk loads outstanding
+   * (so the DMA of step s+1 has landed) and the barrier publishes it. */
+  auto step = [&](auto kk, uint32_t s, const Raw (&wc)[2 * RF], Raw (&wn)[2 * RF]) {
+    constexpr int P = decltype(kk)::value & 1;
+    const uint8_t *Xc = Xb + P * kTileBytes;
+    typename Op::Sc sc[2 * RF];
+#pragma unroll
+    for (int q = 0; q < 2 * RF; ++q) {
+      const uint32_t c = 4u * s + 2u * (uint32_t)(q & 1) + (uint32_t)g;
+      sc[q] = Op::template scale<P>(wc[q], c, c < nchunks);
+    }
+    auto opsB = [&](int k, uint4 (&b)[JT]) {
+      const int pos = (4 * (2 * (k >> 2) + g) + (k & 3)) ^ (r & 15);
+#pragma unroll
+      for (int j = 0; j < JT; ++j)
+        b[j] = *reinterpret_cast<const uint4 *>(Xc + (32 * j + r) * 256 + pos * 16);
+    };
+    auto opsA = [&](int k, uint4 (&A)[RF]) {
+#pragma unroll
+      for (int i = 0; i < RF; ++i) A[i] = Op::word(wc[2 * i + (k >> 2)], k & 3, sc[2 * i + (k >> 2)]);
+    };
+    uint4 Ac[RF], bc[JT];
+    opsB(0, bc);
+    opsA(0, Ac);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint4 An[RF], bn[JT];
+      if (k < 7) opsB(k + 1, bn);
+#pragma unroll
+      for (int j = 0; j < JT; ++j)
+#pragma unroll
+        for (int i = 0; i < RF; ++i) acc[i][j] = mfma<BF>(Ac[i], bc[j], acc[i][j]);
+#ifndef PAI_GEMM_NO_SCHED
+      if (k < 7) {
+        /* order: the next sub-step's LDS reads, then each MFMA followed by
+         * a few VALU operations (its dequantization work) */
+        __builtin_amdgcn_sched_group_barrier(0x100, JT, 0);
+#pragma unroll
+        for (int q = 0; q < RF * JT; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+      }
+#endif
+      if (k == 1) {
+        /* issued after the first waits on this step's chunks, so those
+         * waits do not cover them */
+        dma_x(s + 1u, P ^ 1);
+        load_w(s + 2u, wn);
+      }
+      if (k < 7) {
+        opsA(k + 1, An);
+#pragma unroll
+        for (int i = 0; i < RF; ++i) Ac[i] = An[i];
+#pragma unroll
+        for (int j = 0; j < JT; ++j) bc[j] = bn[j];
+      }
+    }
+    wait_vmem<kWLoads>();
+    __syncthreads();
+  };
+
+  Raw w0[2 * RF], w1[2 * RF], w2[2 * RF], w3[2 * RF];
+  dma_x(s0, 0);
+  load_w(s0, w0);
+  load_w(s0 + 1u, w1);
+  wait_vmem<2 * kWLoads>();
+  __syncthreads();
+  for (uint32_t s = s0; s < s1; s += 4u) {
+    step(std::integral_constant<int, 0>(), s, w0, w2);
+    step(std::integral_constant<int, 1>(), s + 1u, w1, w3);
+    step(std::integral_constant<int, 2>(), s + 2u, w2, w0);
+    step(std::integral_constant<int, 3>(), s + 3u, w3, w1);
+  }
+  wait_vmem<0>(); /* the last steps' requests land before the LDS is reused */
+  __syncthreads();
+
+  const bool split_k = a.splits > 1u;
+  float *Ts = reinterpret_cast<float *>(Xb) + wave * (32 * kTP);
+  constexpr int TPI = 64 / RW;
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
 #pragma unroll
   for (int j = 0; j < JT; ++j) {
@@ -466,20 +720,14 @@ static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <class F, int TT, int NW>
-static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y, bool bf16,
-                            hipStream_t s) {
-  GemmArgs a;
-  a.v = v;
-  a.x = x;
-  a.y = y;
-  a.m = m;
-  a.tiles_n = (v.n + kRowsWG - 1u) / kRowsWG;
-  a.tiles_m = (m + TT - 1u) / TT;
+/* Grid of a launch: tiles of RWG rows x TT tokens; K split while the grid
+ * would leave most of the 256 CUs idle (at least 8 steps per split), the
+ * step count per split a multiple of 4. */
+static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
+  a.tiles_n = (a.v.n + rwg - 1u) / rwg;
+  a.tiles_m = (a.m + tt - 1u) / tt;
   const uint32_t tiles = a.tiles_n * a.tiles_m;
-  const uint32_t nsteps = ((v.k >> 5) + 3u) >> 2;
-  /* split K while the grid would leave most CUs idle (256 CUs), keeping
-   * at least 8 steps per split */
+  const uint32_t nsteps = ((a.v.k >> 5) + 3u) >> 2;
   uint32_t splits = 1;
   while (tiles * splits * 2u <= 256u && nsteps / (splits * 2u) >= 8u) splits *= 2u;
   if (const char *e = getenv("PAI_GEMM_SPLITS")) {
@@ -489,33 +737,87 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
   a.steps_per_split = (nsteps + splits - 1u) / splits;
   a.steps_per_split = (a.steps_per_split + 3u) & ~3u; /* the loop runs steps in fours */
   a.splits = (nsteps + a.steps_per_split - 1u) / a.steps_per_split;
-  const uint32_t total = tiles * a.splits;
-  a.per_xcd = (total + kXcds - 1u) / kXcds;
+  a.per_xcd = (tiles * a.splits + kXcds - 1u) / kXcds;
+}
+
+template <class F, int TT, int NW, int RWG, int XB>
+static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y, bool bf16,
+                            hipStream_t s) {
+  GemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.v = v;
+  a.x = x;
+  a.y = y;
+  a.m = m;
+  plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 4u);
   if (a.splits > 1u) {
     const hipError_t e = zero_fill(y, (size_t)m * v.n, s);
     if (e != hipSuccess) return e;
   }
   const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
-  if (bf16) k_gemm<F, true, TT, NW><<<grid, block, 0, s>>>(a);
-  else k_gemm<F, false, TT, NW><<<grid, block, 0, s>>>(a);
+  if (bf16) k_gemm<F, true, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
+  else k_gemm<F, false, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+template <class F, int TT, int NW, int RWG>
+static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, uint16_t *x16,
+                             float *y, bool bf16, hipStream_t s) {
+  const size_t n4 = (size_t)m * v.k / 4u;
+  const size_t blocks = (n4 + 255u) / 256u;
+  k_cvt_x<<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
+      reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(x16), n4, bf16 ? 1 : 0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  GemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.v = v;
+  a.x16 = x16;
+  a.y = y;
+  a.m = m;
+  plan_grid(a, RWG, TT);
+  a.x_bytes = (uint32_t)((size_t)m * v.k * 2u);
+  if (a.splits > 1u) {
+    e = zero_fill(y, (size_t)m * v.n, s);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
+  if (bf16) k_gemm_x16<F, true, TT, NW, RWG><<<grid, block, 0, s>>>(a);
+  else k_gemm_x16<F, false, TT, NW, RWG><<<grid, block, 0, s>>>(a);
   return hipGetLastError();
 }
 
 template <class F>
 static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x, float *y,
-                              bool bf16, hipStream_t s) {
+                              bool bf16, uint16_t *x16, size_t x16_bytes, hipStream_t s) {
   /* token blocks whose activations span less than 2^31 bytes (32-bit
-   * buffer offsets) */
+   * buffer offsets) and, on the 16-bit path, fit the workspace */
   const size_t row_bytes = (size_t)v.k * 4u;
-  uint32_t blk = (uint32_t)((0x7FFFFFFFu / row_bytes) & ~127u);
-  if (blk == 0u) return hipErrorInvalidValue; /* k > 4M columns */
+  uint32_t blk = (uint32_t)((0x7FFFFFFFu / row_bytes) & ~255u);
+  if (blk == 0u) return hipErrorInvalidValue; /* k > 2M columns */
+  const bool use16 = x16 != nullptr && x16_bytes >= (size_t)v.k * 2u * 256u;
+  if (use16) {
+    const uint32_t fit = (uint32_t)((x16_bytes / ((size_t)v.k * 2u)) & ~(size_t)255u);
+    if (fit < blk) blk = fit;
+  }
   for (uint32_t t0 = 0; t0 < m; t0 += blk) {
     const uint32_t mt = m - t0 < blk ? m - t0 : blk;
     const float *xt = x + (size_t)t0 * v.k;
     float *yt = y + (size_t)t0 * v.n;
-    const hipError_t e = mt <= 32u ? launch_tt<F, 32, kGemmWaves>(v, mt, xt, yt, bf16, s)
-                                   : launch_tt<F, 128, kGemmWaves>(v, mt, xt, yt, bf16, s);
+    /* up to 32 tokens: 32-token tiles; up to 255: 128 x 256 tiles on 8
+     * waves; from 256 tokens: 256 x 128 tiles on 4 waves (each weight
+     * value dequantized once per 256 tokens) */
+    hipError_t e;
+    if (use16) {
+      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(v, mt, xt, x16, yt, bf16, s)
+          : mt < 256u ? launch_x16<F, 128, 8, 256>(v, mt, xt, x16, yt, bf16, s)
+                      : launch_x16<F, 256, 4, 128>(v, mt, xt, x16, yt, bf16, s);
+    } else {
+      e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(v, mt, xt, yt, bf16, s)
+          : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(v, mt, xt, yt, bf16, s)
+                      : launch_tt<F, 256, 4, 128, 1>(v, mt, xt, yt, bf16, s);
+    }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -526,13 +828,15 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
 using namespace paik;
 
 extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
-                              int bf16, void *stream) {
+                              int bf16, void *x16, uint64_t x16_bytes, void *stream) {
   hipStream_t s = (hipStream_t)stream;
+  uint16_t *w16 = static_cast<uint16_t *>(x16);
+  const size_t wb = (size_t)x16_bytes;
   switch (v->type) {
-  case 8u: return (int)launch_gemm<Q8_0>(*v, m, x, y, bf16 != 0, s);
-  case 2u: return (int)launch_gemm<Q4_0>(*v, m, x, y, bf16 != 0, s);
-  case 12u: return (int)launch_gemm<Q4_K>(*v, m, x, y, bf16 != 0, s);
-  case 14u: return (int)launch_gemm<Q6_K>(*v, m, x, y, bf16 != 0, s);
+  case 8u: return (int)launch_gemm<Q8_0>(*v, m, x, y, bf16 != 0, w16, wb, s);
+  case 2u: return (int)launch_gemm<Q4_0>(*v, m, x, y, bf16 != 0, w16, wb, s);
+  case 12u: return (int)launch_gemm<Q4_K>(*v, m, x, y, bf16 != 0, w16, wb, s);
+  case 14u: return (int)launch_gemm<Q6_K>(*v, m, x, y, bf16 != 0, w16, wb, s);
   default: return (int)hipErrorInvalidValue;
   }
 }

@@ -163,7 +163,7 @@ def test_small_batch_parity(qtype, m):
 
 # ------------------------------------------------------------------ MFMA path
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
-@pytest.mark.parametrize("m", [32, 33, 64, 100])
+@pytest.mark.parametrize("m", [32, 33, 64, 100, 300])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_mfma_parity(qtype, m, bf16):
     n, k = 200, 3 * 256
@@ -232,6 +232,24 @@ def test_mfma_forced_split_k_ragged(monkeypatch, splits):
         x = pa.normal_f32(91 + splits, m * k).reshape(m, k)
         y = pa.QMat(qtype, n, k, blocks).gemm(x)
         assert rel_l2(y, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
+
+
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("m", [40, 300])
+def test_mfma_16bit_copy_matches_register_staging(monkeypatch, qtype, m):
+    """The activations reach LDS either from the matrix's 16-bit workspace
+    (DMA) or through registers; both round x the same way and accumulate in
+    the same order, so the outputs are identical."""
+    n, k = 300, 32 * 37 if QK[qtype] == 32 else 256 * 5
+    say(f"[gpu] gemm MFMA x16 vs registers type={qtype} m={m}")
+    blocks = weights(qtype, n, k, 120 + qtype)
+    x = pa.normal_f32(121 + m, m * k).reshape(m, k)
+    qm = pa.QMat(qtype, n, k, blocks)
+    y16 = qm.gemm(x)
+    monkeypatch.setenv("PAI_GEMM_NO_X16", "1")
+    yreg = qm.gemm(x)
+    assert np.array_equal(y16, yreg)
+    assert rel_l2(y16, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
 
 
 # ------------------------------------------------------------------ device pointers
