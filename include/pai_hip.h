@@ -18,8 +18,10 @@
  * HIP failures map to PAI_ERR_INIT / NOMEM / INTERNAL / TIMEOUT.
  *
  * Thread-safety: init/shutdown are idempotent and serialised internally.
- * Calls on different pai_qmat_t handles may run concurrently; the
- * synchronous entry points use one internal stream per calling thread.
+ * Calls on different pai_qmat_t handles may run concurrently; calls on
+ * one handle must not overlap (the handle owns the MFMA path's activation
+ * workspace). The synchronous entry points run on the default stream and
+ * wait for it; their host-pointer staging buffer is shared under a lock.
  */
 #ifndef PAI_HIP_H
 #define PAI_HIP_H
@@ -65,8 +67,8 @@ typedef int32_t pai_status_t;
  * this path; runtime/runtime.c:17-81 is the CPU analogue). */
 pai_status_t pai_hip_init(void);
 
-/* Release the per-thread streams. Idempotent. Handles stay valid only
- * until their pai_qmat_free. */
+/* Release the host-pointer staging buffer. Idempotent. Handles stay valid
+ * until their pai_qmat_free (which also frees their workspace). */
 pai_status_t pai_hip_shutdown(void);
 
 /* Human-readable text of the last failure on this thread ("" if none). */
@@ -121,16 +123,18 @@ uint64_t pai_qmat_bytes(const pai_qmat_t *w);
 
 /* flags for pai_qgemm_f32 / pai_qdequant_f32 */
 #define PAI_QGEMM_DEVICE_PTRS (1u << 0) /* x, y (out) are device pointers  */
-#define PAI_QGEMM_MFMA_BF16 (1u << 1)   /* M >= 32: bf16 MFMA operands      */
+#define PAI_QGEMM_MFMA_BF16 (1u << 1)   /* M >= 8: bf16 MFMA operands       */
 #define PAI_QGEMM_FP32 (1u << 2)        /* any M: f32 dequant + f32 FMA path */
 
 /* y[m][n] = sum_k x[m][k] * W[n][k], x: [M][K] f32, y: [M][N] f32.
- *  - M < 32 (or PAI_QGEMM_FP32): blocks are dequantized in registers and
- *    multiplied in f32 with f32 accumulation. Matches the reference's
- *    sequential f32 sum within rel-L2 1e-5.
- *  - M >= 32: dequantized tiles are staged in LDS as fp16 (default) or
- *    bf16 and multiplied on MFMA with f32 accumulation. Tolerance:
- *    rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16).
+ *  - M < 8 (or PAI_QGEMM_FP32): blocks are multiplied with exact integer
+ *    dot products against a 24-bit image of x and f32 accumulation.
+ *    Matches the reference's sequential f32 sum within rel-L2 1e-5.
+ *  - M >= 8: blocks are dequantized in registers to fp16 (default) or
+ *    bf16, x is rounded to the same type, and MFMA accumulates in f32.
+ *    Tolerance: rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16). Each matrix keeps
+ *    a device workspace for a 16-bit copy of up to 1024 tokens of x,
+ *    allocated by the first such call made outside stream capture.
  * Without PAI_QGEMM_DEVICE_PTRS, x and y are host pointers and the call
  * copies them; with it, they are device pointers. Synchronous.
  * Replaces pai_ref_gemm_f32 at scheduler/scheduler.c:340 for a weight
@@ -150,10 +154,10 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
  * of one layer). All matrices must have the same type and K (otherwise
  * PAI_ERR_MISMATCH). x and every y_i are device pointers; `stream` is a
  * hipStream_t (NULL = the default stream); the call returns once the
- * kernels are enqueued. For M < 32 (or PAI_QGEMM_FP32) the matrices are
+ * kernels are enqueued. For M < 8 (or PAI_QGEMM_FP32) the matrices are
  * multiplied in one launch per group of up to 4 tokens, which streams all
  * of their blocks and converts x once; results are bit-identical to
- * separate pai_qgemm_f32_async calls. For M >= 32 each matrix takes the
+ * separate pai_qgemm_f32_async calls. For M >= 8 each matrix takes the
  * MFMA path of pai_qgemm_f32_async.
  * No counterpart in the reference, whose executor runs each projection as
  * its own pai_ref_gemm_f32 (scheduler/scheduler.c:340); this is the fused

@@ -323,7 +323,7 @@ uint64_t pai_qmat_bytes(const pai_qmat_t *w) { return w != NULL ? w->packed_byte
 /* Compute                                                                  */
 /* ---------------------------------------------------------------------- */
 
-#define PAI_MFMA_MIN_M 32u
+#define PAI_MFMA_MIN_M 8u
 
 /* Workspace of the MFMA path: a 16-bit copy of up to PAI_X16_TOKENS tokens
  * of activations, owned by the matrix handle (calls on one handle do not

@@ -23,7 +23,7 @@ BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
 FLAG_DEVICE_PTRS = 1 << 0
 FLAG_MFMA_BF16 = 1 << 1
 FLAG_FP32 = 1 << 2
-MFMA_MIN_M = 32
+MFMA_MIN_M = 8
 
 
 def qtype_bytes(qtype: int, numel: int) -> int:

@@ -3,9 +3,9 @@ through the C-ABI.
 
 Bars:
   dequant                      bit-exact (NaN outputs compared as NaN)
-  M < 32 and PAI_QGEMM_FP32    rel-L2 <= 1e-5 vs the reference's sequential
+  M < 8 and PAI_QGEMM_FP32     rel-L2 <= 1e-5 vs the reference's sequential
                                f32 operator (and vs the f64 oracle)
-  M >= 32 MFMA                 rel-L2 <= 2e-3 (fp16 operands), 1.6e-2 (bf16)
+  M >= 8 MFMA                  rel-L2 <= 2e-3 (fp16 operands), 1.6e-2 (bf16)
                                vs the f64 oracle
 """
 import ctypes as C
@@ -149,7 +149,7 @@ def test_gemv_q8_0_config1_and_q6_k_down():
 
 # ------------------------------------------------------------------ small batch
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
-@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 31])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 7])
 def test_small_batch_parity(qtype, m):
     n, k = 300, 2 * QK[qtype] * (8 if QK[qtype] == 32 else 1)
     say(f"[gpu] gemm M={m} type={qtype} n={n} k={k}")
@@ -163,7 +163,7 @@ def test_small_batch_parity(qtype, m):
 
 # ------------------------------------------------------------------ MFMA path
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
-@pytest.mark.parametrize("m", [32, 33, 64, 100, 300])
+@pytest.mark.parametrize("m", [8, 31, 32, 33, 64, 100, 300])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_mfma_parity(qtype, m, bf16):
     n, k = 200, 3 * 256
