@@ -20,9 +20,11 @@ cpu_baseline = the reference's AVX2+FMA GEMV (cpu/optimized/opt_ops.c,
            compiled from its sources into oracle/_ref; this repository's
            restatement when that build is absent) on the dequantized f32
            weights of the same seven projections, one host core.
-extra    = the seven projections as separate launches, Q4_K at M in
-           {1, 8, 32}, Q8_0 4096x4096 GEMV, and the M=512 prefill GEMMs
-           (gate Q4_K, down Q6_K) in TFLOP/s against 2.5 PFLOP/s dense fp16.
+extra    = the seven projections as separate launches; the step with
+           silu(gate)*up fused into the gate/up launch; Q4_K at M in
+           {1, 8, 32}; Q8_0 4096x4096 GEMV; and the M=512 prefill GEMMs
+           (gate Q4_K, down Q6_K, and gate+up with the fused silu*mul) in
+           TFLOP/s against 2.5 PFLOP/s dense fp16.
 """
 from __future__ import annotations
 
@@ -78,6 +80,26 @@ def quantized_layer(pa, qtype: int, config: int) -> list:
 # FFN input); o and down stand alone.
 FUSED_STEP = [("qkv", [0, 1, 2]), ("o", [3]), ("gate_up", [4, 5]), ("down", [6])]
 SEPARATE_STEP = [(name, [i]) for i, (name, _, _) in enumerate(PROJ)]
+# The same step with the FFN activation fused into the gate/up launch:
+# h = silu(gate) * up is written instead of the two products.
+SILU_STEP = [("qkv", [0, 1, 2]), ("o", [3]), ("gate_up_silu", [4, 5]), ("down", [6])]
+
+
+def enqueue_entry(pa, layer, name, idx, m, xp, yp, sh):
+    if name == "gate_up_silu":
+        pa.gate_up_async(layer.w[idx[0]], layer.w[idx[1]], xp, yp[idx[0]], m, 0, sh)
+    elif len(idx) == 1:
+        layer.w[idx[0]].gemm_async(xp, yp[idx[0]], m, 0, sh)
+    else:
+        pa.gemm_multi_async([layer.w[i] for i in idx], xp, [yp[i] for i in idx], m, 0, sh)
+
+
+def entry_bytes(pa, qtype, name, idx, m):
+    """Algorithmic bytes of one plan entry: packed weights, x once, outputs."""
+    if name == "gate_up_silu":
+        n, k = PROJ[idx[0]][1], PROJ[idx[0]][2]
+        return len(idx) * n * pa.qtype_bytes(qtype, k) + m * (k + n) * 4
+    return sum(call_bytes(pa, qtype, PROJ[i][1], PROJ[i][2], m) for i in idx)
 
 
 def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, plan):
@@ -95,11 +117,8 @@ def run_layers(pa, hm, layers, m: int, steps: int, warmup: int, plan):
     xp, yp = x.ptr, [y.ptr for y in ys]
 
     def enqueue(layer, sh):
-        for _, idx in plan:
-            if len(idx) == 1:
-                layer.w[idx[0]].gemm_async(xp, yp[idx[0]], m, 0, sh)
-            else:
-                pa.gemm_multi_async([layer.w[i] for i in idx], xp, [yp[i] for i in idx], m, 0, sh)
+        for name, idx in plan:
+            enqueue_entry(pa, layer, name, idx, m, xp, yp, sh)
 
     nl = len(layers)
     for l in layers:  # eager pass first: per-matrix workspaces are allocated outside capture
@@ -142,12 +161,10 @@ def per_launch_times(pa, hm, layers, m: int, plan, reps: int = 50) -> dict:
     out = {}
     for name, idx in plan:
         def one(sh, r):
-            layer = layers[r % len(layers)]
-            if len(idx) == 1:
-                layer.w[idx[0]].gemm_async(x.ptr, ys[idx[0]].ptr, m, 0, sh)
-            else:
-                pa.gemm_multi_async([layer.w[i] for i in idx], x.ptr, [ys[i].ptr for i in idx],
-                                    m, 0, sh)
+            enqueue_entry(pa, layers[r % len(layers)], name, idx, m, x.ptr,
+                          [y.ptr for y in ys], sh)
+        one(stream.handle, 0)  # eager first: workspaces are allocated outside capture
+        stream.synchronize()
         g = hm.Graph(stream, lambda sh: [one(sh, r) for r in range(reps)])
         g.launch(stream)
         stream.synchronize()
@@ -157,7 +174,7 @@ def per_launch_times(pa, hm, layers, m: int, plan, reps: int = 50) -> dict:
         b.record(stream)
         b.synchronize()
         us = a.elapsed_ms(b) * 1e3 / reps
-        nbytes = sum(call_bytes(pa, layers[0].qtype, PROJ[i][1], PROJ[i][2], m) for i in idx)
+        nbytes = entry_bytes(pa, layers[0].qtype, name, idx, m)
         out[name] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
         a.destroy(); b.destroy(); g.destroy()
     for buf in [x, *ys]:
@@ -171,7 +188,7 @@ def gemv_config(pa, hm, qtype: int, config: int, m: int, nlayers: int, steps: in
     blocks = quantized_layer(pa, qtype, config)
     layers = [Layer(pa, qtype, blocks) for _ in range(nlayers)]
     wall, gpu_ms = run_layers(pa, hm, layers, m, steps, warmup, plan)
-    bytes_step = sum(call_bytes(pa, qtype, n, k, m) for _, n, k in PROJ)
+    bytes_step = sum(entry_bytes(pa, qtype, name, idx, m) for name, idx in plan)
     res = {"qtype": qtype, "m": m, "layers": nlayers, "steps": steps,
            "launches_per_step": len(plan),
            "weight_set_MB": round(nlayers * sum(l.nbytes for l in layers[0].w) / 1e6, 1),
@@ -263,6 +280,20 @@ def prefill(pa, hm, reps: int) -> dict:
         out[name] = {"us": round(us, 1), "TFLOPs": round(tflops, 1),
                      "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 3)}
         qm.free(); x.free(); y.free()
+    # gate and up (Q4_K 14336 x 4096) with h = silu(gate) * up fused
+    n, k = 14336, 4096
+    mats = [pa.QMat(pa.Q4_K, n, k, pa.quantize(pa.Q4_K, pa.normal_f32(
+        seed_w(4, i), n * k, 0.0, 0.02).reshape(n, k))) for i in (4, 5)]
+    x = hm.DeviceBuffer.from_array(pa.normal_f32(seed_w(4, 9), m * k))
+    h = hm.DeviceBuffer(m * n * 4)
+    us = timed_calls(hm, lambda sh, i: pa.gate_up_async(mats[0], mats[1], x.ptr, h.ptr, m, 0, sh),
+                     reps, 3)
+    tflops = 2.0 * 2.0 * m * n * k / (us * 1e-6) / 1e12
+    out["gate_up_silu_q4_k"] = {"us": round(us, 1), "TFLOPs": round(tflops, 1),
+                                "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 3)}
+    for w in mats:
+        w.free()
+    x.free(); h.free()
     return out
 
 
@@ -420,6 +451,11 @@ def main() -> int:
             extra["q4_0_m1_separate"] = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, 300, 20,
                                                     plan=SEPARATE_STEP)
             log(f"Q4_0 M=1 separate: {extra['q4_0_m1_separate']['gpu_GBps']:.1f} GB/s GPU")
+            extra["q4_0_m1_silu_fused"] = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, 300,
+                                                      20, plan=SILU_STEP)
+            log(f"Q4_0 M=1 with silu*mul fused: "
+                f"{extra['q4_0_m1_silu_fused']['gpu_GBps']:.1f} GB/s GPU; "
+                f"{extra['q4_0_m1_silu_fused']['per_launch']}")
             extra["q4_k_m1"] = gemv_config(pa, hm, pa.Q4_K, 3, 1, args.layers, 300, 20)
             log(f"Q4_K M=1: {extra['q4_k_m1']['gpu_GBps']:.1f} GB/s GPU; "
                 f"{extra['q4_k_m1']['per_launch']}")

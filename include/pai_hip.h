@@ -118,6 +118,69 @@ pai_status_t pai_qmat_shape(const pai_qmat_t *w, uint32_t *type, uint64_t *n,
 uint64_t pai_qmat_bytes(const pai_qmat_t *w);
 
 /* ---------------------------------------------------------------------- */
+/* GGUF files: tensor directory and upload without dequantization          */
+/* ---------------------------------------------------------------------- */
+
+/* Read-only tensor directory over a GGUF file held in memory (for example
+ * mmap'ed). It does not own the buffer, which must outlive it. */
+typedef struct pai_gguf_dir pai_gguf_dir_t;
+
+/* Parse the header, metadata and tensor infos. Accepts exactly the files
+ * pai_gguf_open accepts (adapters/llama/gguf.h:76-78, gguf.c:128-245) with
+ * the same codes: PROTOCOL for malformed input (short file, bad magic,
+ * reads past the end, unknown metadata type, empty or >= 128-byte names,
+ * n_dims outside 1..4, extents above 2^26, a bad alignment, a data section
+ * past the end), UNSUPPORTED for versions outside 1..3 or more than 1024
+ * tensors; NOMEM, INVALID_ARG for NULL. Metadata values are skipped, except
+ * "general.alignment". */
+pai_status_t pai_gguf_dir_open(const void *data, uint64_t size,
+                               pai_gguf_dir_t **out);
+
+/* Free the directory (not the buffer). NULL is a no-op. */
+void pai_gguf_dir_close(pai_gguf_dir_t *d);
+
+/* Number of tensors (pai_gguf_t.tensor_count); 0 for NULL. */
+uint64_t pai_gguf_dir_count(const pai_gguf_dir_t *d);
+
+/* File version, alignment and byte offset of the data section from the
+ * start of the buffer (pai_gguf_t.version / .alignment / .data_start).
+ * Any output may be NULL. */
+pai_status_t pai_gguf_dir_layout(const pai_gguf_dir_t *d, uint32_t *version,
+                                 uint32_t *alignment, uint64_t *data_start);
+
+/* Tensor info `index` (0-based, file order): the fields of
+ * pai_gguf_tensor_t (adapters/llama/gguf.h:54-60). `name` stays valid until
+ * pai_gguf_dir_close; dims receives 4 extents, innermost first, unused ones
+ * 0; offset is relative to the data section. Any output may be NULL.
+ * INVALID_ARG for an index out of range. */
+pai_status_t pai_gguf_dir_tensor(const pai_gguf_dir_t *d, uint64_t index,
+                                 const char **name, uint32_t *type,
+                                 uint32_t *n_dims, uint64_t *dims,
+                                 uint64_t *offset);
+
+/* Index of the first tensor named exactly `name`; MISMATCH when absent
+ * (pai_gguf_find_tensor, adapters/llama/gguf.h:98-99, returns NULL). */
+pai_status_t pai_gguf_dir_find(const pai_gguf_dir_t *d, const char *name,
+                               uint64_t *index);
+
+/* Pointer into the buffer at tensor `index`'s native blocks and their byte
+ * count, after the checks pai_gguf_dequant makes before reading them
+ * (adapters/llama/gguf.c:984-996): PROTOCOL for zero elements or bytes
+ * outside the file, UNSUPPORTED for a type other than the four block
+ * formats or an element count that is not whole blocks. */
+pai_status_t pai_gguf_dir_blocks(const pai_gguf_dir_t *d, uint64_t index,
+                                 const void **blocks, uint64_t *nbytes);
+
+/* Upload the 2-D tensor `name` (extents [K, N], innermost first) as a
+ * resident matrix W[N][K], straight from its native blocks: no dequant, no
+ * transpose. Replaces, for GPU sessions, the per-tensor import in
+ * adapters/llama/llama.c:408-470 (pai_gguf_find_tensor, pai_gguf_dequant,
+ * transpose2d). Errors: MISMATCH (absent, or not 2-D), then those of
+ * pai_gguf_dir_blocks and pai_qmat_upload. */
+pai_status_t pai_qmat_upload_gguf(pai_qmat_t **out, const pai_gguf_dir_t *d,
+                                  const char *name);
+
+/* ---------------------------------------------------------------------- */
 /* Compute                                                                  */
 /* ---------------------------------------------------------------------- */
 
@@ -166,6 +229,27 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
 pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t count,
                                        uint64_t m, const float *x, float *const *ys,
                                        uint32_t flags, void *stream);
+
+/* Feed-forward gate/up with its activation fused:
+ *   h[m][N] = silu(x W_gate^T) * (x W_up^T),  silu(g) = g / (1 + e^-g).
+ * Replaces the reference's four ops GEMM(gate), GEMM(up), SILU, MUL
+ * (adapters/llama/llama.c:760-784, executed at scheduler/scheduler.c:340,
+ * :484-488, :404-410); the gate and up products are never written out.
+ * W_gate and W_up must have the same type, N and K (PAI_ERR_MISMATCH).
+ * x and h are device pointers; `stream` as for pai_qgemm_f32_async.
+ *  - M < 8 (or PAI_QGEMM_FP32): one launch per group of up to 4 tokens
+ *    streams both matrices and applies the epilogue in registers; each
+ *    token's gate and up sums are those pai_qgemm_f32_async computes for
+ *    that token alone (M = 1), bit for bit, and silu uses the device expf
+ *    (within 4 ulp of the reference's f32 composition applied to them).
+ *    K up to 18720 (PAI_ERR_UNSUPPORTED above).
+ *  - M >= 8: the gate product is written to h, then the up product's
+ *    epilogue replaces each element by silu(h) * up (that launch is not
+ *    split over K). Tolerances of the MFMA path. */
+pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate,
+                                         const pai_qmat_t *w_up, uint64_t m,
+                                         const float *x, float *h,
+                                         uint32_t flags, void *stream);
 
 /* out[N][K] = dequantized W in the native element order, computed on the
  * GPU from the device copy; bit-identical to pai_gguf_dequant

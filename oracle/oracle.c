@@ -331,6 +331,21 @@ int32_t orc_qgemm_f64(uint32_t type, uint64_t n, uint64_t k,
   return ORC_OK;
 }
 
+/* h[i] = silu(g[i]) * u[i]: pai_ref_silu_f32 (cpu/reference/ref_ops.c:
+ * 219-228, g / (1 + expf(-g)) with the C library's expf) followed by
+ * pai_ref_vecmul_f32 (ref_ops.c:124-133), the SILU and MUL ops of the
+ * reference's FFN (adapters/llama/llama.c:774-784). */
+int32_t orc_silu_mul_f32(const float *g, const float *u, float *h, uint64_t n) {
+  if ((g == NULL || u == NULL || h == NULL) && n != 0u) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    const float s = g[i] / (1.0f + expf(-g[i]));
+    h[i] = s * u[i];
+  }
+  return ORC_OK;
+}
+
 /* |a-b| <= max(abs_tol, |b|*rel_tol) per element; first failing index.
  * Follows cpu/reference/ref_ops.c:518-541. */
 int32_t orc_compare_f32(const float *a, const float *b, uint64_t n,

@@ -25,6 +25,10 @@
  *   orc_qgemm_seq_f32     composition of the two above; one-hot x returns
  *                         a dequantized column exactly.
  *   orc_qgemm_f64         closed-form sums on tiny shapes.
+ *   orc_silu_mul_f32      the reference's pai_ref_silu_f32 and
+ *                         pai_ref_vecmul_f32 built into oracle/_ref
+ *                         (bit-exact), and silu's closed-form points
+ *                         (silu(0) = 0, silu(x) -> x, silu(-x) -> -0).
  *   orc_opt_gemv_avx2 /   the reference's opt_ops.c built into oracle/_ref
  *   orc_opt_gemm_w8_avx2  (bit-exact), and tolerance vs the f64 oracle.
  *   orc_q8_0_encode_ref / textbook llama.cpp encoders used to pin the
@@ -69,6 +73,7 @@ int32_t orc_qgemm_seq_f32(uint32_t type, uint64_t n, uint64_t k,
 int32_t orc_qgemm_f64(uint32_t type, uint64_t n, uint64_t k,
                       const uint8_t *blocks, uint64_t m, const float *x,
                       double *y);
+int32_t orc_silu_mul_f32(const float *g, const float *u, float *h, uint64_t n);
 int32_t orc_compare_f32(const float *a, const float *b, uint64_t n,
                         float abs_tol, float rel_tol, uint64_t *first_bad);
 

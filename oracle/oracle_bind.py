@@ -30,6 +30,7 @@ _ORACLE_SIGS = {
     "orc_qgemm_f64": (C.c_int32, [C.c_uint32, C.c_uint64, C.c_uint64, _vp, C.c_uint64, _vp,
                                   _vp]),
     "orc_compare_f32": (C.c_int32, [_vp, _vp, C.c_uint64, C.c_float, C.c_float, _vp]),
+    "orc_silu_mul_f32": (C.c_int32, [_vp, _vp, _vp, C.c_uint64]),
     "orc_opt_gemv_avx2": (C.c_int32, [C.c_uint64, C.c_uint64, _vp, _vp, _vp]),
     "orc_opt_gemv_avx2_mt": (C.c_int32, [C.c_uint64, C.c_uint64, _vp, _vp, _vp, C.c_int]),
     "orc_opt_gemm_avx2": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
@@ -45,6 +46,8 @@ _REF_SIGS = {
     "pai_gguf_dequant": (C.c_int32, [_vp, _vp, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
     "pai_gguf_type_bytes": (C.c_uint64, [C.c_uint32, C.c_uint64]),
     "pai_ref_gemm_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
+    "pai_ref_silu_f32": (C.c_int32, [_vp, _vp, C.c_uint64]),
+    "pai_ref_vecmul_f32": (C.c_int32, [_vp, _vp, _vp, C.c_uint64]),
     "pai_opt_gemv_f32": (C.c_int32, [C.c_uint64, C.c_uint64, _vp, _vp, _vp]),
     "pai_opt_gemm_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
     "pai_opt_gemm_w8_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
@@ -130,6 +133,16 @@ def qgemm_f64(qtype: int, n: int, k: int, blocks: np.ndarray, x: np.ndarray) -> 
     return y
 
 
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    h = np.empty_like(g)
+    st = oracle().orc_silu_mul_f32(_p(g), _p(u), _p(h), g.size)
+    if st != 0:
+        raise RuntimeError(f"orc_silu_mul_f32 status {st}")
+    return h
+
+
 # ---------------------------------------------------------------- reference wrappers
 def gguf_image(qtype: int, dims: tuple, raw: bytes) -> bytes:
     """A one-tensor GGUF v3 file image (name "t", dims innermost first,
@@ -167,3 +180,61 @@ def ref_dequant(qtype: int, raw: bytes, numel: int, row: int | None = None) -> n
         return arr
     finally:
         r.pai_gguf_close(f)
+
+
+class RefGGUFTensor(C.Structure):
+    """pai_gguf_tensor_t (adapters/llama/gguf.h:54-60)."""
+    _fields_ = [("name", C.c_char * 128), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("type", C.c_uint32), ("offset", C.c_uint64)]
+
+
+class RefGGUF(C.Structure):
+    """pai_gguf_t (adapters/llama/gguf.h:62-73)."""
+    _fields_ = [("data", C.c_void_p), ("size", C.c_uint64), ("version", C.c_uint32),
+                ("tensor_count", C.c_uint64), ("kv_count", C.c_uint64),
+                ("alignment", C.c_uint64), ("kv_start", C.c_void_p),
+                ("data_start", C.c_void_p), ("tensors", C.POINTER(RefGGUFTensor))]
+
+
+def ref_gguf_directory(img: bytes):
+    """pai_gguf_open from the reference build on a file image. Returns
+    (status, layout, tensors): layout = (version, alignment, data_start
+    offset); tensors = [(name, type, n_dims, dims, offset)]."""
+    r = ref()
+    buf = C.create_string_buffer(bytes(img), max(len(img), 1))
+    f = RefGGUF()
+    st = r.pai_gguf_open(buf, len(img), C.byref(f))
+    if st != 0:
+        return st, None, None
+    try:
+        base = C.addressof(buf)
+        layout = (f.version, f.alignment, f.data_start - base)
+        ts = []
+        for i in range(f.tensor_count):
+            t = f.tensors[i]
+            ts.append((t.name.decode(errors="surrogateescape"), t.type, t.n_dims, tuple(t.dims), t.offset))
+        return st, layout, ts
+    finally:
+        r.pai_gguf_close(C.byref(f))
+
+
+def ref_gguf_dequant_status(img: bytes, name: str) -> int:
+    """Status of pai_gguf_dequant for tensor `name` of a file image the
+    reference opens."""
+    r = ref()
+    buf = C.create_string_buffer(bytes(img), max(len(img), 1))
+    f = RefGGUF()
+    st = r.pai_gguf_open(buf, len(img), C.byref(f))
+    if st != 0:
+        raise RuntimeError(f"pai_gguf_open status {st}")
+    try:
+        t = r.pai_gguf_find_tensor(C.byref(f), name.encode())
+        if not t:
+            raise RuntimeError(f"no tensor {name}")
+        out, n = C.c_void_p(), C.c_uint64()
+        st = r.pai_gguf_dequant(C.byref(f), t, C.byref(out), C.byref(n))
+        if out.value:
+            _libc.free(out)
+        return st
+    finally:
+        r.pai_gguf_close(C.byref(f))

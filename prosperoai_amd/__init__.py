@@ -6,12 +6,14 @@ The product is the C-ABI library prosperoai_amd/lib/libpai_hip.so
 and benchmarks.
 """
 from ._lib import LIB_PATH, PaiError, check, lib
+from .gguf import GGUFDir, TensorInfo
 from .qmat import (BLOCK_BYTES, BLOCK_ELEMS, FLAG_DEVICE_PTRS, FLAG_FP32, FLAG_MFMA_BF16,
                    MFMA_MIN_M, Q4_0, Q4_K, Q6_K, Q8_0, QTYPES, QMat, descriptors,
-                   gemm_multi_async, init, normal_f32, qtype_bytes, quantize)
+                   gate_up_async, gemm_multi_async, init, normal_f32, qtype_bytes, quantize)
 
 __all__ = [
     "LIB_PATH", "PaiError", "check", "lib", "BLOCK_BYTES", "BLOCK_ELEMS", "FLAG_DEVICE_PTRS",
     "FLAG_FP32", "FLAG_MFMA_BF16", "MFMA_MIN_M", "Q4_0", "Q4_K", "Q6_K", "Q8_0", "QTYPES",
-    "QMat", "descriptors", "gemm_multi_async", "init", "normal_f32", "qtype_bytes", "quantize",
+    "QMat", "GGUFDir", "TensorInfo", "descriptors", "gate_up_async", "gemm_multi_async", "init",
+    "normal_f32", "qtype_bytes", "quantize",
 ]

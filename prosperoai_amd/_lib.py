@@ -36,7 +36,21 @@ SIGNATURES = {
     "pai_qgemm_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32, _vp]),
     "pai_qgemm_f32_multi_async": (C.c_int32, [C.POINTER(C.c_void_p), C.c_uint32, C.c_uint64, _vp,
                                               C.POINTER(C.c_void_p), C.c_uint32, _vp]),
+    "pai_qgemm_f32_gate_up_async": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp, C.c_uint32,
+                                                _vp]),
     "pai_qdequant_f32": (C.c_int32, [_vp, _vp, C.c_uint32]),
+    "pai_gguf_dir_open": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_void_p)]),
+    "pai_gguf_dir_close": (None, [_vp]),
+    "pai_gguf_dir_count": (C.c_uint64, [_vp]),
+    "pai_gguf_dir_layout": (C.c_int32, [_vp, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                        C.POINTER(C.c_uint64)]),
+    "pai_gguf_dir_tensor": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_char_p),
+                                        C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                        C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "pai_gguf_dir_find": (C.c_int32, [_vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "pai_gguf_dir_blocks": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_void_p),
+                                        C.POINTER(C.c_uint64)]),
+    "pai_qmat_upload_gguf": (C.c_int32, [C.POINTER(C.c_void_p), _vp, C.c_char_p]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),
     "pai_hip_op_name": (C.c_char_p, [C.c_uint32]),
     # paiq.h

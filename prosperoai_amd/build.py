@@ -23,7 +23,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-C_SOURCES = ["pai_hip.c", "paiq.c"]
+C_SOURCES = ["pai_hip.c", "pai_gguf.c", "paiq.c"]
 HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemm.hip"]
 HEADERS = ["paik.h", "qdev.h"]
 

@@ -38,13 +38,16 @@ struct pai_qmat {
 
 static _Thread_local char t_err[256];
 
-static pai_status_t fail(pai_status_t st, const char *fmt, ...) {
+/* Shared with pai_gguf.c; not exported from the library. */
+__attribute__((visibility("hidden"))) pai_status_t pai__fail(pai_status_t st, const char *fmt,
+                                                             ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(t_err, sizeof t_err, fmt, ap);
   va_end(ap);
   return st;
 }
+#define fail pai__fail
 
 const char *pai_hip_last_error(void) { return t_err; }
 
@@ -364,18 +367,22 @@ static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint
   return p;
 }
 
+static pai_status_t launch_mfma(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
+                                const float *gate, uint32_t flags, hipStream_t s) {
+  uint64_t wb = 0;
+  void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(w, m, s, &wb);
+  const int e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, gate,
+                               (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, s);
+  return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+}
+
 static pai_status_t launch(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
                            uint32_t flags, hipStream_t s) {
-  int e;
   if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
-    e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
-  } else {
-    uint64_t wb = 0;
-    void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(w, m, s, &wb);
-    e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb,
-                       s);
+    const int e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
+    return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
-  return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+  return launch_mfma(w, m, x, y, NULL, flags, s);
 }
 
 static pai_status_t check_call(const pai_qmat_t *w, uint64_t m, const void *x, const void *y) {
@@ -422,6 +429,32 @@ pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t cou
     if (st != PAI_OK) return st;
   }
   return PAI_OK;
+}
+
+pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qmat_t *w_up,
+                                         uint64_t m, const float *x, float *h, uint32_t flags,
+                                         void *stream) {
+  pai_status_t st = check_call(w_gate, m, x, h);
+  if (st != PAI_OK) return st;
+  st = check_call(w_up, m, x, h);
+  if (st != PAI_OK) return st;
+  if (w_up->type != w_gate->type || w_up->n != w_gate->n || w_up->k != w_gate->k)
+    return fail(PAI_ERR_MISMATCH, "gate and up differ in type or shape");
+  if (((uintptr_t)x & 15u) != 0u || ((uintptr_t)h & 3u) != 0u)
+    return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned, h 4-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
+    if (w_gate->k > paik_gemv_pair_max_k())
+      return fail(PAI_ERR_UNSUPPORTED, "K=%llu above %u for the fused gate/up product at M < %u",
+                  (unsigned long long)w_gate->k, paik_gemv_pair_max_k(), PAI_MFMA_MIN_M);
+    const int e = paik_gemv_silu_mul(&w_gate->view, &w_up->view, (uint32_t)m, x, h, s);
+    return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+  }
+  /* the gate product lands in h; the up product's epilogue turns each
+   * element into silu(gate) * up in place */
+  st = launch_mfma(w_gate, m, x, h, NULL, flags, s);
+  if (st != PAI_OK) return st;
+  return launch_mfma(w_up, m, x, h, h, flags, s);
 }
 
 pai_status_t pai_qgemm_f32(const pai_qmat_t *w, uint64_t m, const float *x, float *y,

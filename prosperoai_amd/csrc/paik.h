@@ -64,11 +64,18 @@ int paik_gemv(const paik_qview_t *v, uint32_t m, const float *x, float *y,
  * count, in one launch per group of up to 4 tokens. */
 int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys,
                     uint32_t count, uint32_t m, const float *x, void *stream);
+/* h = silu(x W_gate^T) * (x W_up^T) in one launch per token group
+ * (gate and up of one type and shape; K up to paik_gemv_pair_max_k()). */
+int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
+                       uint32_t m, const float *x, float *h, void *stream);
+uint32_t paik_gemv_pair_max_k(void);
 /* x16 (may be NULL): device workspace of x16_bytes for a 16-bit copy of
- * the activations; with it the activations move into LDS by DMA. */
+ * the activations; with it the activations move into LDS by DMA.
+ * gate (may be NULL, may equal y): y = silu(gate) * (x W^T) elementwise,
+ * gate being [m][n]; such launches are not split over K. */
 int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
-                   float *y, int bf16, void *x16, uint64_t x16_bytes,
-                   void *stream);
+                   float *y, const float *gate, int bf16, void *x16,
+                   uint64_t x16_bytes, void *stream);
 
 #ifdef __cplusplus
 }

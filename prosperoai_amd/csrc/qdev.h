@@ -78,6 +78,12 @@ __device__ __forceinline__ uint32_t word4(const uint4 &q, int j) {
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+/* silu(g) * u in the reference's order of operations: g / (1 + e^-g)
+ * (cpu/reference/ref_ops.c:219-228), then the product
+ * (pai_ref_vecmul_f32, the MUL op at scheduler/scheduler.c:404-410).
+ * expf is the device library's; the division is IEEE. */
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
 struct QRes {
   __amdgpu_buffer_rsrc_t q, aux, meta, d;
   uint32_t q_stride, nb, k4;

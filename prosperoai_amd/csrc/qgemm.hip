@@ -245,6 +245,10 @@ struct GemmArgs {
   const float *x;
   const uint16_t *x16; /* activations already rounded to 16 bits (k_gemm_x16) */
   float *y;
+  /* when set: y = silu(gate) * (x W^T), gate[M][N] the gate projection's
+   * output (may be y itself; each element is read before it is written by
+   * the same thread), and the launch is not split over K */
+  const float *gate;
   uint32_t m;
   uint32_t tiles_n, tiles_m, splits; /* grid: tiles_n * tiles_m * splits (padded to kXcds) */
   uint32_t per_xcd;                  /* workgroups per XCD */
@@ -459,9 +463,10 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
       const float val = Ts[tt * kTP + lane % RW];
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
-        float *dst = a.y + (size_t)tok * v.n + orow;
-        if (split_k) unsafeAtomicAdd(dst, val);
-        else *dst = val;
+        const size_t at = (size_t)tok * v.n + orow;
+        if (split_k) unsafeAtomicAdd(a.y + at, val);
+        else if (a.gate != nullptr) a.y[at] = silu_mul(a.gate[at], val);
+        else a.y[at] = val;
       }
     }
   }
@@ -688,9 +693,10 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
       const float val = Ts[tt * kTP + lane % RW];
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
-        float *dst = a.y + (size_t)tok * v.n + orow;
-        if (split_k) unsafeAtomicAdd(dst, val);
-        else *dst = val;
+        const size_t at = (size_t)tok * v.n + orow;
+        if (split_k) unsafeAtomicAdd(a.y + at, val);
+        else if (a.gate != nullptr) a.y[at] = silu_mul(a.gate[at], val);
+        else a.y[at] = val;
       }
     }
   }
@@ -734,6 +740,7 @@ static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
     const int r = atoi(e);
     if (r >= 1 && r <= 64) splits = (uint32_t)r;
   }
+  if (a.gate != nullptr) splits = 1u; /* the epilogue needs whole sums */
   a.steps_per_split = (nsteps + splits - 1u) / splits;
   a.steps_per_split = (a.steps_per_split + 3u) & ~3u; /* the loop runs steps in fours */
   a.splits = (nsteps + a.steps_per_split - 1u) / a.steps_per_split;
@@ -741,13 +748,14 @@ static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
 }
 
 template <class F, int TT, int NW, int RWG, int XB>
-static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y, bool bf16,
-                            hipStream_t s) {
+static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y,
+                            const float *gate, bool bf16, hipStream_t s) {
   GemmArgs a;
   memset(&a, 0, sizeof a);
   a.v = v;
   a.x = x;
   a.y = y;
+  a.gate = gate;
   a.m = m;
   plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 4u);
@@ -763,7 +771,7 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
 
 template <class F, int TT, int NW, int RWG>
 static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, uint16_t *x16,
-                             float *y, bool bf16, hipStream_t s) {
+                             float *y, const float *gate, bool bf16, hipStream_t s) {
   const size_t n4 = (size_t)m * v.k / 4u;
   const size_t blocks = (n4 + 255u) / 256u;
   k_cvt_x<<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
@@ -775,6 +783,7 @@ static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, 
   a.v = v;
   a.x16 = x16;
   a.y = y;
+  a.gate = gate;
   a.m = m;
   plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 2u);
@@ -790,7 +799,8 @@ static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, 
 
 template <class F>
 static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x, float *y,
-                              bool bf16, uint16_t *x16, size_t x16_bytes, hipStream_t s) {
+                              const float *gate, bool bf16, uint16_t *x16, size_t x16_bytes,
+                              hipStream_t s) {
   /* token blocks whose activations span less than 2^31 bytes (32-bit
    * buffer offsets) and, on the 16-bit path, fit the workspace */
   const size_t row_bytes = (size_t)v.k * 4u;
@@ -805,18 +815,19 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
     const uint32_t mt = m - t0 < blk ? m - t0 : blk;
     const float *xt = x + (size_t)t0 * v.k;
     float *yt = y + (size_t)t0 * v.n;
+    const float *gt = gate != nullptr ? gate + (size_t)t0 * v.n : nullptr;
     /* up to 32 tokens: 32-token tiles; up to 255: 128 x 256 tiles on 8
      * waves; from 256 tokens: 256 x 128 tiles on 4 waves (each weight
      * value dequantized once per 256 tokens) */
     hipError_t e;
     if (use16) {
-      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(v, mt, xt, x16, yt, bf16, s)
-          : mt < 256u ? launch_x16<F, 128, 8, 256>(v, mt, xt, x16, yt, bf16, s)
-                      : launch_x16<F, 256, 4, 128>(v, mt, xt, x16, yt, bf16, s);
+      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(v, mt, xt, x16, yt, gt, bf16, s)
+          : mt < 256u ? launch_x16<F, 128, 8, 256>(v, mt, xt, x16, yt, gt, bf16, s)
+                      : launch_x16<F, 256, 4, 128>(v, mt, xt, x16, yt, gt, bf16, s);
     } else {
-      e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(v, mt, xt, yt, bf16, s)
-          : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(v, mt, xt, yt, bf16, s)
-                      : launch_tt<F, 256, 4, 128, 1>(v, mt, xt, yt, bf16, s);
+      e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(v, mt, xt, yt, gt, bf16, s)
+          : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(v, mt, xt, yt, gt, bf16, s)
+                      : launch_tt<F, 256, 4, 128, 1>(v, mt, xt, yt, gt, bf16, s);
     }
     if (e != hipSuccess) return e;
   }
@@ -828,15 +839,17 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
 using namespace paik;
 
 extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
-                              int bf16, void *x16, uint64_t x16_bytes, void *stream) {
+                              const float *gate, int bf16, void *x16, uint64_t x16_bytes,
+                              void *stream) {
   hipStream_t s = (hipStream_t)stream;
   uint16_t *w16 = static_cast<uint16_t *>(x16);
   const size_t wb = (size_t)x16_bytes;
+  const bool b = bf16 != 0;
   switch (v->type) {
-  case 8u: return (int)launch_gemm<Q8_0>(*v, m, x, y, bf16 != 0, w16, wb, s);
-  case 2u: return (int)launch_gemm<Q4_0>(*v, m, x, y, bf16 != 0, w16, wb, s);
-  case 12u: return (int)launch_gemm<Q4_K>(*v, m, x, y, bf16 != 0, w16, wb, s);
-  case 14u: return (int)launch_gemm<Q6_K>(*v, m, x, y, bf16 != 0, w16, wb, s);
+  case 8u: return (int)launch_gemm<Q8_0>(*v, m, x, y, gate, b, w16, wb, s);
+  case 2u: return (int)launch_gemm<Q4_0>(*v, m, x, y, gate, b, w16, wb, s);
+  case 12u: return (int)launch_gemm<Q4_K>(*v, m, x, y, gate, b, w16, wb, s);
+  case 14u: return (int)launch_gemm<Q6_K>(*v, m, x, y, gate, b, w16, wb, s);
   default: return (int)hipErrorInvalidValue;
   }
 }

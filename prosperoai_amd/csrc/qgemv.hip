@@ -26,10 +26,11 @@
  *      then two cross-row steps). The summation order is fixed by the
  *      launch shape, so results do not depend on scheduling.
  *
- * Rows longer than one slice (the chunks whose planes fit the 64 KiB LDS
- * budget: 512 chunks = 16384 columns at MT = 1, U = 4) are covered by
- * successive launches over column slices; all but the first add into y
- * (each output is read and written by one lane, in launch order).
+ * Rows longer than one slice (the chunk-tokens whose planes fit the 64 KiB
+ * LDS budget: 585, i.e. rows up to 18720 columns at MT = 1, 9344 at MT = 2
+ * and 4672 at MT = 4) are covered by successive launches over column
+ * slices of a multiple of 64 chunks; all but the first add into y (each
+ * output is read and written by one lane, in launch order).
  *
  * The integer sums are exact; the roundings are the 24-bit image of x
  * (<= 2^-23 of the chunk's largest |x|), the per-chunk scale steps and the
@@ -137,7 +138,8 @@ __device__ __forceinline__ void plane_words(const float v[8], uint32_t jw, XSlot
  * memory results are consumed in issue order: an activation load issued
  * after the weight ring would wait for all of it). Four consecutive
  * threads share a chunk; a thread takes up to kXIt chunk quarters, which
- * covers a slice of up to kXIt * 512 / 4 = 512 chunk-tokens. */
+ * covers up to kXIt * 1024 / 4 = 1024 chunk-tokens (more than the LDS
+ * budget holds). */
 constexpr int kXIt = 4;
 constexpr uint32_t kMaxSliceTok = (uint32_t)kXIt * 64u * kWaves / 4u;
 
@@ -180,7 +182,10 @@ __device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[kXIt],
 /* Matrices of one launch: up to kMaxMats weights with the same format and
  * column count, multiplied by the same activations (the q/k/v or gate/up
  * projections of a layer). Waves [wave_end[i-1], wave_end[i]) work on
- * matrix i, so no wave's rows cross a matrix boundary. */
+ * matrix i, so no wave's rows cross a matrix boundary.
+ * Paired launches (the PAIR kernels) instead take v[0] = gate and v[1] = up
+ * of one row count and write y[0] = silu(x W_gate^T) * (x W_up^T): every
+ * wave works on both matrices over the same rows. */
 constexpr int kMaxMats = 4;
 struct GemvArgs {
   paik_qview_t v[kMaxMats];
@@ -198,11 +203,15 @@ struct GemvArgs {
  * add with a non-returning atomic (each output has one writer per launch,
  * and launches on a stream run in order, so the result is the same as a
  * read-add-write). */
-template <class F, int U, int MT>
+template <class F, int U, int MT, bool PAIR>
 __global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *__restrict__ x,
                                                       uint32_t ntok, uint32_t cs, uint32_t nsc,
                                                       int accumulate) {
   static_assert(U * MT <= 16, "at most 16 outputs per row group");
+  static_assert(!PAIR || U % 2 == 0, "a paired row group holds gate and up rows");
+  /* output rows per row group; in a paired launch slot u of a group holds
+   * row u/2 of matrix u%2 */
+  constexpr int UR = PAIR ? U / 2 : U;
   extern __shared__ uint4 smem[];
   XSlot *xp = reinterpret_cast<XSlot *>(smem);
   XScale *xf = reinterpret_cast<XScale *>(xp + (size_t)MT * nsc);
@@ -214,37 +223,44 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *_
   const uint32_t gw = blockIdx.x * (uint32_t)kWaves + wave;
   /* the matrix this wave works on, and its share of that matrix's rows */
   uint32_t mi = 0, w0 = 0;
+  if constexpr (!PAIR) {
 #pragma unroll
-  for (int i = 1; i < kMaxMats; ++i)
-    if ((uint32_t)i < a.count && gw >= a.wave_end[i - 1]) {
-      mi = (uint32_t)i;
-      w0 = a.wave_end[i - 1];
-    }
+    for (int i = 1; i < kMaxMats; ++i)
+      if ((uint32_t)i < a.count && gw >= a.wave_end[i - 1]) {
+        mi = (uint32_t)i;
+        w0 = a.wave_end[i - 1];
+      }
+  }
   paik_qview_t v = a.v[0];
   float *y = a.y[0];
+  if constexpr (!PAIR) {
 #pragma unroll
-  for (int i = 1; i < kMaxMats; ++i)
-    if (mi == (uint32_t)i) {
-      v = a.v[i];
-      y = a.y[i];
-    }
+    for (int i = 1; i < kMaxMats; ++i)
+      if (mi == (uint32_t)i) {
+        v = a.v[i];
+        y = a.y[i];
+      }
+  }
   const uint64_t lw = gw - w0, tw = a.wave_end[mi] - w0;
   const uint32_t r_beg = (uint32_t)(lw * v.n / tw), r_end = (uint32_t)((lw + 1u) * v.n / tw);
   const uint32_t steps = (nsc + 63u) >> 6;
-  const uint32_t groups = (r_end - r_beg + (uint32_t)U - 1u) / (uint32_t)U;
+  const uint32_t groups = (r_end - r_beg + (uint32_t)UR - 1u) / (uint32_t)UR;
   const uint32_t nblk = groups * steps; /* wave-uniform; 0 for a wave without rows */
   const uint32_t blk_last = nblk > 0u ? nblk - 1u : 0u;
   const uint32_t row_last = r_end > r_beg ? r_end - 1u : min(r_beg, v.n - 1u);
 
   const QRes res = make_qres(v);
+  const QRes res_up = make_qres(a.v[PAIR ? 1 : 0]);
   auto load_block = [&](uint32_t b, typename F::Raw (&buf)[U]) {
     const uint32_t bb = min(b, blk_last);
     const uint32_t g = bb / steps, s = bb % steps;
     const uint32_t cb = cs + 64u * s;                /* wave-uniform chunk base */
     const uint32_t ln = min(lane, nsc - 1u - 64u * s); /* cb + ln stays in the slice */
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      buf[u] = F::bload(res, min(r_beg + g * (uint32_t)U + (uint32_t)u, row_last), cb, ln);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t row = min(r_beg + g * (uint32_t)UR + (uint32_t)(PAIR ? u / 2 : u), row_last);
+      buf[u] = F::bload((PAIR && (u & 1)) ? res_up : res, row, cb, ln);
+    }
   };
 
   /* Activation loads first, then the ring of PD blocks (kInFlight
@@ -272,7 +288,7 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *_
     const uint32_t cl = 64u * s + lane;
     const bool live = cl < nsc;
     const uint32_t clc = min(cl, nsc - 1u);
-    const uint32_t row0 = r_beg + g * (uint32_t)U;
+    const uint32_t row0 = r_beg + g * (uint32_t)UR;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       XChunk xc;
@@ -292,10 +308,25 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *_
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const float d = F::dot(buf[u], cs + clc, xc);
-        acc[u][t] += (live && row0 + (uint32_t)u < r_end) ? d : 0.0f;
+        acc[u][t] += (live && row0 + (uint32_t)(PAIR ? u / 2 : u) < r_end) ? d : 0.0f;
       }
     }
-    if (s + 1u == steps) {
+    if (PAIR && s + 1u == steps) {
+      /* paired row group done: lane j = p*MT + t combines row p's gate and
+       * up sums for token t (a paired launch covers the whole row) */
+#pragma unroll
+      for (int p = 0; p < UR; ++p)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const float sg = group_sum<64>(acc[2 * p][t]);
+          const float su = group_sum<64>(acc[2 * p + 1][t]);
+          acc[2 * p][t] = 0.0f;
+          acc[2 * p + 1][t] = 0.0f;
+          const uint32_t row = row0 + (uint32_t)p;
+          if (lane == (uint32_t)(p * MT + t) && row < r_end && (uint32_t)t < ntok)
+            y[(size_t)t * v.n + row] = silu_mul(sg, su);
+        }
+    } else if (s + 1u == steps) {
       /* Row group done: every output's 64 lane partials are summed in
        * registers (DPP within 16-lane rows, then two cross-row steps); lane
        * j then writes output j = u*MT + t. */
@@ -372,19 +403,27 @@ static void split_waves(GemvArgs &a, uint32_t total_waves) {
   }
 }
 
-template <class F, int U, int MT>
+/* Chunks of one column slice: those whose activation planes for MT
+ * tokens fit the LDS budget and one pass of the plane builder. */
+static uint32_t slice_cap(uint32_t mt) {
+  const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)mt * (sizeof(XSlot) + sizeof(XScale))));
+  return min(fit, kMaxSliceTok / mt);
+}
+
+template <class F, int U, int MT, bool PAIR>
 static hipError_t launch_u(GemvArgs a, const float *x, uint32_t ntok, uint32_t grid,
                            hipStream_t s) {
   const uint32_t nchunks = a.v[0].k >> 5;
-  const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)MT * (sizeof(XSlot) + sizeof(XScale))));
-  const uint32_t cap = min(fit, kMaxSliceTok / (uint32_t)MT);
+  const uint32_t cap = slice_cap((uint32_t)MT);
   const uint32_t slice = cap >= nchunks ? nchunks : (cap & ~63u);
-  split_waves(a, grid * (uint32_t)kWaves);
+  if (PAIR && slice != nchunks) return hipErrorInvalidValue; /* the epilogue needs whole rows */
+  if constexpr (PAIR) a.wave_end[0] = grid * (uint32_t)kWaves;
+  else split_waves(a, grid * (uint32_t)kWaves);
   for (uint32_t cs = 0; cs < nchunks; cs += slice) {
     const uint32_t nsc = min(slice, nchunks - cs);
     const size_t lds = (size_t)MT * nsc * (sizeof(XSlot) + sizeof(XScale));
-    k_gemv<F, U, MT><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(a, x, ntok, cs, nsc,
-                                                                 cs != 0u ? 1 : 0);
+    k_gemv<F, U, MT, PAIR><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(a, x, ntok, cs, nsc,
+                                                                       cs != 0u ? 1 : 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -398,17 +437,31 @@ static hipError_t launch_gemv(const GemvArgs &a, const float *x, uint32_t ntok, 
   const uint32_t grid = pick_grid(rows, a.count);
   const int u = pick_rows<MT>(rows, grid);
   if constexpr (MT == 1) {
-    if (u == 4) return launch_u<F, 4, 1>(a, x, ntok, grid, s);
-    if (u == 2) return launch_u<F, 2, 1>(a, x, ntok, grid, s);
-    return launch_u<F, 1, 1>(a, x, ntok, grid, s);
+    if (u == 4) return launch_u<F, 4, 1, false>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 1, false>(a, x, ntok, grid, s);
+    return launch_u<F, 1, 1, false>(a, x, ntok, grid, s);
   } else if constexpr (MT == 2) {
-    if (u == 4) return launch_u<F, 4, 2>(a, x, ntok, grid, s);
-    if (u == 2) return launch_u<F, 2, 2>(a, x, ntok, grid, s);
-    return launch_u<F, 1, 2>(a, x, ntok, grid, s);
+    if (u == 4) return launch_u<F, 4, 2, false>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 2, false>(a, x, ntok, grid, s);
+    return launch_u<F, 1, 2, false>(a, x, ntok, grid, s);
   } else {
-    if (u == 2) return launch_u<F, 2, MT>(a, x, ntok, grid, s);
-    return launch_u<F, 1, MT>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, MT, false>(a, x, ntok, grid, s);
+    return launch_u<F, 1, MT, false>(a, x, ntok, grid, s);
   }
+}
+
+/* Paired gate/up launch: grid sized for both matrices' rows; a row group
+ * holds 2 rows of each matrix when waves get 2 or more rows (and MT <= 2),
+ * else 1. */
+template <class F, int MT>
+static hipError_t launch_pair(const GemvArgs &a, const float *x, uint32_t ntok, hipStream_t s) {
+  const uint32_t n = a.v[0].n;
+  const uint32_t grid = pick_grid(2u * n, 1u);
+  const uint32_t rw = (n + grid * kWaves - 1u) / (grid * kWaves);
+  if constexpr (MT <= 2) {
+    if (rw >= 2u) return launch_u<F, 4, MT, true>(a, x, ntok, grid, s);
+  }
+  return launch_u<F, 2, MT, true>(a, x, ntok, grid, s);
 }
 
 template <class F>
@@ -434,9 +487,51 @@ static hipError_t gemv_tokens(const paik_qview_t *const *vs, float *const *ys, u
   return hipSuccess;
 }
 
+/* h = silu(x W_gate^T) * (x W_up^T), in token groups whose activation
+ * planes fit one slice (so every output is finished in one launch). */
+template <class F>
+static hipError_t gemv_pair_tokens(const paik_qview_t *vg, const paik_qview_t *vu, uint32_t m,
+                                   const float *x, float *h, hipStream_t s) {
+  const uint32_t nchunks = vg->k >> 5;
+  const uint32_t group = slice_cap(4u) >= nchunks ? 4u : slice_cap(2u) >= nchunks ? 2u : 1u;
+  if (slice_cap(group) < nchunks) return hipErrorInvalidValue;
+  for (uint32_t t0 = 0; t0 < m; t0 += group) {
+    const uint32_t nt = m - t0 < group ? m - t0 : group;
+    GemvArgs a;
+    memset(&a, 0, sizeof a);
+    a.count = 2;
+    a.v[0] = *vg;
+    a.v[1] = *vu;
+    a.y[0] = h + (size_t)t0 * vg->n;
+    const float *xt = x + (size_t)t0 * vg->k;
+    hipError_t e;
+    if (nt == 1u) e = launch_pair<F, 1>(a, xt, 1u, s);
+    else if (nt == 2u) e = launch_pair<F, 2>(a, xt, 2u, s);
+    else e = launch_pair<F, 4>(a, xt, nt, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 } // namespace paik
 
 using namespace paik;
+
+extern "C" uint32_t paik_gemv_pair_max_k(void) { return slice_cap(1u) * 32u; }
+
+extern "C" int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up, uint32_t m,
+                                  const float *x, float *h, void *stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (gate->type != up->type || gate->n != up->n || gate->k != up->k)
+    return (int)hipErrorInvalidValue;
+  switch (gate->type) {
+  case 8u: return (int)gemv_pair_tokens<Q8_0>(gate, up, m, x, h, s);
+  case 2u: return (int)gemv_pair_tokens<Q4_0>(gate, up, m, x, h, s);
+  case 12u: return (int)gemv_pair_tokens<Q4_K>(gate, up, m, x, h, s);
+  case 14u: return (int)gemv_pair_tokens<Q6_K>(gate, up, m, x, h, s);
+  default: return (int)hipErrorInvalidValue;
+  }
+}
 
 extern "C" int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                                uint32_t m, const float *x, void *stream) {

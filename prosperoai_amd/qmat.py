@@ -74,6 +74,16 @@ class QMat:
             check(lib().pai_qmat_upload(C.byref(self._h), qtype, n, k, b.ctypes.data, b.nbytes),
                   "pai_qmat_upload")
 
+    @classmethod
+    def adopt(cls, handle: C.c_void_p) -> "QMat":
+        """Wrap a handle made by another upload entry point (it is freed with the object)."""
+        self = cls.__new__(cls)
+        self._h = handle
+        t, n, k = C.c_uint32(), C.c_uint64(), C.c_uint64()
+        check(lib().pai_qmat_shape(handle, C.byref(t), C.byref(n), C.byref(k)), "pai_qmat_shape")
+        self.qtype, self.n, self.k = t.value, n.value, k.value
+        return self
+
     @property
     def handle(self) -> int:
         return self._h.value
@@ -122,3 +132,11 @@ def gemm_multi_async(mats: list, x_ptr: int, y_ptrs: list, m: int, flags: int = 
     ys = (C.c_void_p * n)(*y_ptrs)
     check(lib().pai_qgemm_f32_multi_async(hs, n, m, x_ptr, ys, flags | FLAG_DEVICE_PTRS,
                                           stream or None), "pai_qgemm_f32_multi_async")
+
+
+def gate_up_async(w_gate: QMat, w_up: QMat, x_ptr: int, h_ptr: int, m: int, flags: int = 0,
+                  stream: int = 0) -> None:
+    """h = silu(x W_gate^T) * (x W_up^T) (pai_qgemm_f32_gate_up_async; device pointers)."""
+    check(lib().pai_qgemm_f32_gate_up_async(w_gate.handle, w_up.handle, m, x_ptr, h_ptr,
+                                            flags | FLAG_DEVICE_PTRS, stream or None),
+          "pai_qgemm_f32_gate_up_async")

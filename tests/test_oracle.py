@@ -239,3 +239,42 @@ def test_compare_semantics():
     assert bad.value == 1
     assert ob.oracle().orc_compare_f32(a.ctypes.data, b.ctypes.data, 3, 0.2, 0.0,
                                        C.addressof(bad)) == 0
+
+
+def _silu_mul_inputs():
+    rng = np.random.default_rng(31)
+    g = np.concatenate([rng.normal(0, 3, 4000), rng.normal(0, 40, 1000),
+                        [0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, 89.0, -104.0, -110.0, 1e30,
+                         -1e30, np.inf, -np.inf]]).astype(np.float32)
+    u = rng.normal(0, 1, g.size).astype(np.float32)
+    return g, u
+
+
+def test_silu_mul_matches_reference_build(ref_lib):
+    """orc_silu_mul_f32 is the reference's SILU then MUL, bit for bit
+    (cpu/reference/ref_ops.c:219-228 and :124-133)."""
+    g, u = _silu_mul_inputs()
+    s, want = np.empty_like(g), np.empty_like(g)
+    assert ref_lib.pai_ref_silu_f32(g.ctypes.data, s.ctypes.data, g.size) == 0
+    assert ref_lib.pai_ref_vecmul_f32(s.ctypes.data, u.ctypes.data, want.ctypes.data, g.size) == 0
+    got = ob.silu_mul(g, u)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_silu_mul_closed_form():
+    g, u = _silu_mul_inputs()
+    h = ob.silu_mul(g, np.ones_like(u))
+    fin = np.isfinite(g) & (np.abs(g) < 1e29)
+    # against the f64 closed form g / (1 + e^-g): a few ulp, where e^-g
+    # stays finite in f32 (below g = -88.7 the f32 composition gives -0)
+    fin &= g > -87.0
+    ref = g[fin].astype(np.float64) / (1.0 + np.exp(-g[fin].astype(np.float64)))
+    assert np.all(np.abs(h[fin] - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-38)
+    # fixed points: silu(0) = 0, silu(x) = x for large x, -> -0 for very negative x
+    assert h[g == 0].tolist() == [0.0, 0.0]
+    assert h[g == 89.0][0] == 89.0 and h[g == 1e30][0] == 1e30
+    assert h[g == -110.0][0] == 0.0 and np.signbit(h[g == -110.0][0])
+    assert np.isnan(h[g == -np.inf][0]) and h[g == np.inf][0] == np.inf
+    # the product is the elementwise one
+    fin = np.isfinite(g) & (np.abs(g) < 1e29)
+    assert np.array_equal(ob.silu_mul(g, u)[fin], (h * u)[fin])
