@@ -24,7 +24,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 C_SOURCES = ["pai_hip.c", "pai_gguf.c", "paiq.c"]
-HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemm.hip"]
+HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemv_mx.hip", "qgemm.hip"]
 HEADERS = ["paik.h", "qdev.h"]
 
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",

@@ -327,6 +327,27 @@ uint64_t pai_qmat_bytes(const pai_qmat_t *w) { return w != NULL ? w->packed_byte
 /* ---------------------------------------------------------------------- */
 
 #define PAI_MFMA_MIN_M 8u
+/* Token count from which calls take the 16-bit MFMA GEMM; below it the
+ * GEMV kernels (PAI_MFMA_MIN_M, or the PAI_MFMA_MIN_M environment value
+ * for measurements). */
+static uint64_t mfma_min_m(void) {
+  static uint64_t v = 0;
+  if (v == 0) {
+    const char *e = getenv("PAI_MFMA_MIN_M");
+    const long r = e ? atol(e) : 0;
+    v = r >= 2 && r <= 4096 ? (uint64_t)r : PAI_MFMA_MIN_M;
+  }
+  return v;
+}
+
+/* Calls that take the GEMV kernels: under mfma_min_m() tokens, the
+ * PAI_QGEMM_FP32 flag, or up to 8 tokens that one launch of the
+ * matrix-core GEMV covers (its weight operands serve every token, so it
+ * streams W once where the 16-bit GEMM adds conversion and fill launches). */
+static int gemv_call(const pai_qmat_t *w, uint64_t m, uint32_t flags) {
+  if (m < mfma_min_m() || (flags & PAI_QGEMM_FP32) != 0u) return 1;
+  return m <= 8u && paik_gemv_mx_tokens((uint32_t)w->k, (uint32_t)m) >= m;
+}
 
 /* Workspace of the MFMA path: a 16-bit copy of up to PAI_X16_TOKENS tokens
  * of activations, owned by the matrix handle (calls on one handle do not
@@ -378,7 +399,7 @@ static pai_status_t launch_mfma(const pai_qmat_t *w, uint64_t m, const float *x,
 
 static pai_status_t launch(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
                            uint32_t flags, hipStream_t s) {
-  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
+  if (gemv_call(w, m, flags)) {
     const int e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
@@ -418,7 +439,7 @@ pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t cou
   }
   if (((uintptr_t)x & 15u) != 0u) return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
+  if (gemv_call(ws[0], m, flags)) {
     const paik_qview_t *vs[PAI_MULTI_MAX];
     for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
     const int e = paik_gemv_multi(vs, ys, count, (uint32_t)m, x, s);
@@ -443,8 +464,11 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
   if (((uintptr_t)x & 15u) != 0u || ((uintptr_t)h & 3u) != 0u)
     return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned, h 4-byte aligned");
   hipStream_t s = (hipStream_t)stream;
-  if (m < PAI_MFMA_MIN_M || (flags & PAI_QGEMM_FP32) != 0u) {
-    if (w_gate->k > paik_gemv_pair_max_k())
+  if (gemv_call(w_gate, m, flags)) {
+    /* one token, or a K the matrix-core GEMV does not take: the integer-dot
+     * kernel, which needs whole rows in one launch */
+    const int mx = m >= 2u && paik_gemv_mx_tokens((uint32_t)w_gate->k, (uint32_t)m) != 0u;
+    if (!mx && w_gate->k > paik_gemv_pair_max_k())
       return fail(PAI_ERR_UNSUPPORTED, "K=%llu above %u for the fused gate/up product at M < %u",
                   (unsigned long long)w_gate->k, paik_gemv_pair_max_k(), PAI_MFMA_MIN_M);
     const int e = paik_gemv_silu_mul(&w_gate->view, &w_up->view, (uint32_t)m, x, h, s);

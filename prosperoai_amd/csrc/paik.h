@@ -69,6 +69,15 @@ int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys,
 int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
                        uint32_t m, const float *x, float *h, void *stream);
 uint32_t paik_gemv_pair_max_k(void);
+/* Batched GEMV on the i8 matrix cores (qgemv_mx.hip): y_i = x W_i^T for
+ * count (1..4) matrices of one format and K, or h = silu(x Wg^T) * (x Wu^T),
+ * for m tokens in launches of paik_gemv_mx_tokens(k, m) tokens (1, 2, 4
+ * or 8; 0 when K is not taken: K must be a multiple of 128). */
+uint32_t paik_gemv_mx_tokens(uint32_t k, uint32_t m);
+int paik_gemv_mx(const paik_qview_t *const *vs, float *const *ys,
+                 uint32_t count, uint32_t m, const float *x, void *stream);
+int paik_gemv_mx_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
+                          uint32_t m, const float *x, float *h, void *stream);
 /* x16 (may be NULL): device workspace of x16_bytes for a 16-bit copy of
  * the activations; with it the activations move into LDS by DMA.
  * gate (may be NULL, may equal y): y = silu(gate) * (x W^T) elementwise,

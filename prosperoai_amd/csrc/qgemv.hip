@@ -43,6 +43,7 @@
 namespace paik {
 
 constexpr int kWaves = 16;   /* waves per workgroup (one workgroup per CU) */
+constexpr int kWavesSmall = 8; /* for one-token launches with under 2 rows per wave at kWaves */
 constexpr int kInFlight = 8; /* row-chunk loads per lane kept in flight */
 constexpr size_t kLdsBudget = 65536; /* bytes of LDS per workgroup */
 
@@ -141,7 +142,8 @@ __device__ __forceinline__ void plane_words(const float v[8], uint32_t jw, XSlot
  * covers up to kXIt * 1024 / 4 = 1024 chunk-tokens (more than the LDS
  * budget holds). */
 constexpr int kXIt = 4;
-constexpr uint32_t kMaxSliceTok = (uint32_t)kXIt * 64u * kWaves / 4u;
+/* chunk-tokens one pass of the plane builder covers, per workgroup size */
+__host__ __device__ constexpr uint32_t max_slice_tok(int nw) { return (uint32_t)kXIt * 64u * (uint32_t)nw / 4u; }
 
 template <int MT>
 __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, uint32_t ntok,
@@ -203,8 +205,8 @@ struct GemvArgs {
  * add with a non-returning atomic (each output has one writer per launch,
  * and launches on a stream run in order, so the result is the same as a
  * read-add-write). */
-template <class F, int U, int MT, bool PAIR>
-__global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *__restrict__ x,
+template <class F, int U, int MT, bool PAIR, int NW>
+__global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__restrict__ x,
                                                       uint32_t ntok, uint32_t cs, uint32_t nsc,
                                                       int accumulate) {
   static_assert(U * MT <= 16, "at most 16 outputs per row group");
@@ -220,7 +222,7 @@ __global__ void __launch_bounds__(64 * kWaves) k_gemv(GemvArgs a, const float *_
   /* the wave index is uniform; reading it from lane 0 lets every row and
    * block quantity below live in scalar registers */
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const uint32_t gw = blockIdx.x * (uint32_t)kWaves + wave;
+  const uint32_t gw = blockIdx.x * (uint32_t)NW + wave;
   /* the matrix this wave works on, and its share of that matrix's rows */
   uint32_t mi = 0, w0 = 0;
   if constexpr (!PAIR) {
@@ -405,24 +407,37 @@ static void split_waves(GemvArgs &a, uint32_t total_waves) {
 
 /* Chunks of one column slice: those whose activation planes for MT
  * tokens fit the LDS budget and one pass of the plane builder. */
-static uint32_t slice_cap(uint32_t mt) {
+static uint32_t slice_cap(uint32_t mt, int nw = kWaves) {
   const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)mt * (sizeof(XSlot) + sizeof(XScale))));
-  return min(fit, kMaxSliceTok / mt);
+  return min(fit, max_slice_tok(nw) / mt);
 }
 
-template <class F, int U, int MT, bool PAIR>
+/* One-token launches of up to 4096 rows (two rows per wave on 256
+ * workgroups of 8 waves) run on that grid instead of half as many 16-wave
+ * workgroups, so every CU shares the dot-product work, when a row still
+ * fits one column slice of the smaller plane builder (PAI_GEMV_NW=16 / 8
+ * forces either). */
+static bool small_wg(uint32_t rows, uint32_t k) {
+  static const int nw = getenv("PAI_GEMV_NW") ? atoi(getenv("PAI_GEMV_NW")) : 0;
+  if ((k >> 5) > slice_cap(1u, kWavesSmall)) return false; /* rows stay one slice */
+  if (nw == 16) return false;
+  if (nw == 8) return true;
+  return rows <= kWavesSmall * 2u * 256u;
+}
+
+template <class F, int U, int MT, bool PAIR, int NW = kWaves>
 static hipError_t launch_u(GemvArgs a, const float *x, uint32_t ntok, uint32_t grid,
                            hipStream_t s) {
   const uint32_t nchunks = a.v[0].k >> 5;
-  const uint32_t cap = slice_cap((uint32_t)MT);
+  const uint32_t cap = slice_cap((uint32_t)MT, NW);
   const uint32_t slice = cap >= nchunks ? nchunks : (cap & ~63u);
   if (PAIR && slice != nchunks) return hipErrorInvalidValue; /* the epilogue needs whole rows */
-  if constexpr (PAIR) a.wave_end[0] = grid * (uint32_t)kWaves;
-  else split_waves(a, grid * (uint32_t)kWaves);
+  if constexpr (PAIR) a.wave_end[0] = grid * (uint32_t)NW;
+  else split_waves(a, grid * (uint32_t)NW);
   for (uint32_t cs = 0; cs < nchunks; cs += slice) {
     const uint32_t nsc = min(slice, nchunks - cs);
     const size_t lds = (size_t)MT * nsc * (sizeof(XSlot) + sizeof(XScale));
-    k_gemv<F, U, MT, PAIR><<<dim3(grid), dim3(64u * kWaves), lds, s>>>(a, x, ntok, cs, nsc,
+    k_gemv<F, U, MT, PAIR, NW><<<dim3(grid), dim3(64u * NW), lds, s>>>(a, x, ntok, cs, nsc,
                                                                        cs != 0u ? 1 : 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -437,6 +452,13 @@ static hipError_t launch_gemv(const GemvArgs &a, const float *x, uint32_t ntok, 
   const uint32_t grid = pick_grid(rows, a.count);
   const int u = pick_rows<MT>(rows, grid);
   if constexpr (MT == 1) {
+    if (small_wg(rows, a.v[0].k)) {
+      /* 256 workgroups of kWavesSmall waves, two or more rows per wave */
+      const uint32_t g8 = min(256u, (rows + 2u * kWavesSmall - 1u) / (2u * kWavesSmall));
+      const uint32_t rw = (rows + g8 * kWavesSmall - 1u) / (g8 * kWavesSmall);
+      if (rw >= 4u) return launch_u<F, 4, 1, false, kWavesSmall>(a, x, ntok, g8, s);
+      return launch_u<F, 2, 1, false, kWavesSmall>(a, x, ntok, g8, s);
+    }
     if (u == 4) return launch_u<F, 4, 1, false>(a, x, ntok, grid, s);
     if (u == 2) return launch_u<F, 2, 1, false>(a, x, ntok, grid, s);
     return launch_u<F, 1, 1, false>(a, x, ntok, grid, s);
@@ -464,9 +486,20 @@ static hipError_t launch_pair(const GemvArgs &a, const float *x, uint32_t ntok, 
   return launch_u<F, 2, MT, true>(a, x, ntok, grid, s);
 }
 
+/* Calls of two or more tokens run on the matrix-core kernel (qgemv_mx.hip)
+ * where it takes K: its weight operands are shared by all tokens of a
+ * launch, while this kernel's integer dots are paid per token. One token
+ * stays here, where the dots are cheaper than the matrix-core operand
+ * layout's scattered loads. PAI_GEMV_NO_MX=1 keeps every call here. */
+static bool use_mx(uint32_t k, uint32_t m) {
+  static const bool off = getenv("PAI_GEMV_NO_MX") != nullptr;
+  return !off && m >= 2u && paik_gemv_mx_tokens(k, m) != 0u;
+}
+
 template <class F>
 static hipError_t gemv_tokens(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                               uint32_t m, const float *x, hipStream_t s) {
+  if (use_mx(vs[0]->k, m)) return (hipError_t)paik_gemv_mx(vs, ys, count, m, x, s);
   /* groups of up to 4 tokens per launch; each launch re-streams W */
   for (uint32_t t0 = 0; t0 < m; t0 += 4u) {
     const uint32_t nt = m - t0 < 4u ? m - t0 : 4u;
@@ -492,6 +525,7 @@ static hipError_t gemv_tokens(const paik_qview_t *const *vs, float *const *ys, u
 template <class F>
 static hipError_t gemv_pair_tokens(const paik_qview_t *vg, const paik_qview_t *vu, uint32_t m,
                                    const float *x, float *h, hipStream_t s) {
+  if (use_mx(vg->k, m)) return (hipError_t)paik_gemv_mx_silu_mul(vg, vu, m, x, h, s);
   const uint32_t nchunks = vg->k >> 5;
   const uint32_t group = slice_cap(4u) >= nchunks ? 4u : slice_cap(2u) >= nchunks ? 2u : 1u;
   if (slice_cap(group) < nchunks) return hipErrorInvalidValue;

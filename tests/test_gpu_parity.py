@@ -149,7 +149,7 @@ def test_gemv_q8_0_config1_and_q6_k_down():
 
 # ------------------------------------------------------------------ small batch
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
-@pytest.mark.parametrize("m", [2, 3, 4, 5, 7])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 7, 8])
 def test_small_batch_parity(qtype, m):
     n, k = 300, 2 * QK[qtype] * (8 if QK[qtype] == 32 else 1)
     say(f"[gpu] gemm M={m} type={qtype} n={n} k={k}")
@@ -161,9 +161,36 @@ def test_small_batch_parity(qtype, m):
         assert rel_l2(y[i], ref[i]) <= TOL_F32, i
 
 
+@pytest.mark.parametrize("qtype", [2, 12])
+def test_batched_decode_llama8b_m8(qtype):
+    """Eight tokens at the 8B shapes: q (K = 4096) takes the matrix-core
+    GEMV (one launch covers the tokens), down (K = 14336) the 16-bit GEMM."""
+    m = 8
+    for proj, tol in (("q", TOL_F32), ("gate", TOL_F32), ("down", TOL_F16)):
+        n, k = LLAMA8B[proj]
+        say(f"[gpu] batched decode M=8 type={qtype} proj={proj}")
+        blocks = weights(qtype, n, k, 0xC0DE0100 + list(LLAMA8B).index(proj))
+        x = pa.normal_f32(0xC0DE0100 ^ 0x5A5A, m * k).reshape(m, k)
+        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        rows = np.arange(0, n, 7)
+        ref = ob.qgemm_f64(qtype, len(rows), k, blocks[rows], x)
+        assert rel_l2(y[:, rows], ref) <= tol, proj
+
+
+def test_batched_gemv_longer_rows_fewer_tokens():
+    """K = 14336 holds 2 tokens per matrix-core launch: 5 tokens run as
+    launches of 2, 2 and 1; K = 9344 (73 steps) splits unevenly over waves."""
+    for qtype, n, k, m in ((14, 100, 14336, 5), (2, 64, 9344, 3)):
+        say(f"[gpu] batched gemv type={qtype} k={k} m={m}")
+        blocks = weights(qtype, n, k, 4400 + m)
+        x = pa.normal_f32(4401 + m, m * k).reshape(m, k)
+        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        assert rel_l2(y, ob.qgemm_seq(qtype, n, k, blocks, x)) <= TOL_F32
+
+
 # ------------------------------------------------------------------ MFMA path
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
-@pytest.mark.parametrize("m", [8, 31, 32, 33, 64, 100, 300])
+@pytest.mark.parametrize("m", [12, 31, 32, 33, 64, 100, 300])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_mfma_parity(qtype, m, bf16):
     n, k = 200, 3 * 256
