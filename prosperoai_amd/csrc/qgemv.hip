@@ -154,14 +154,20 @@ __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, 
   for (int it = 0; it < kXIt; ++it) {
     const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
     const uint32_t t = idx / (nsc * 4u), r = idx % (nsc * 4u);
-    /* clamped, unconditional load; tokens >= ntok and idle threads read
-     * token 0's first columns and are zeroed by the select below */
+    /* Idle threads and tokens >= ntok load nothing (zeros). Given a
+     * clamped address instead, every idle thread of every workgroup would
+     * request the same line, which the L2 serves one request at a time:
+     * that held the activations of a 256-workgroup launch for microseconds. */
     const bool ok = idx < total && t < ntok;
-    const float4 *src = reinterpret_cast<const float4 *>(
-        x + (ok ? (size_t)t * k + 32u * (cs + (r >> 2)) + 8u * (r & 3u) : (size_t)32u * cs));
-    const float4 a = src[0], b = src[1];
-    va[it] = make_float4(ok ? a.x : 0.f, ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
-    vb[it] = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (ok) {
+      const float4 *src = reinterpret_cast<const float4 *>(
+          x + (size_t)t * k + 32u * (cs + (r >> 2)) + 8u * (r & 3u));
+      a = src[0];
+      b = src[1];
+    }
+    va[it] = a;
+    vb[it] = b;
   }
 }
 
@@ -253,14 +259,19 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 
   const QRes res = make_qres(v);
   const QRes res_up = make_qres(a.v[PAIR ? 1 : 0]);
+  /* block, row and chunk base are wave-uniform; readfirstlane keeps them
+   * in SGPRs (the buffer offset operand) when the compiler would compute
+   * them on the vector unit */
+  auto rfl = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
   auto load_block = [&](uint32_t b, typename F::Raw (&buf)[U]) {
-    const uint32_t bb = min(b, blk_last);
-    const uint32_t g = bb / steps, s = bb % steps;
-    const uint32_t cb = cs + 64u * s;                /* wave-uniform chunk base */
+    const uint32_t bb = rfl(min(b, blk_last));
+    const uint32_t g = rfl(bb / steps), s = rfl(bb % steps);
+    const uint32_t cb = rfl(cs + 64u * s);             /* wave-uniform chunk base */
     const uint32_t ln = min(lane, nsc - 1u - 64u * s); /* cb + ln stays in the slice */
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t row = min(r_beg + g * (uint32_t)UR + (uint32_t)(PAIR ? u / 2 : u), row_last);
+      const uint32_t row =
+          rfl(min(r_beg + g * (uint32_t)UR + (uint32_t)(PAIR ? u / 2 : u), row_last));
       buf[u] = F::bload((PAIR && (u & 1)) ? res_up : res, row, cb, ln);
     }
   };
@@ -272,9 +283,13 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
   x_load<MT>(x, v.k, ntok, cs, nsc, xa, xb);
   constexpr int PD = kInFlight / U;
   typename F::Raw buf[PD][U];
+  /* Every load below is unconditional (blocks past the wave's last one
+   * re-read that block, an L2 hit), so each wave issues the same sequence
+   * and the compiler's wait before block b's dot products counts exactly
+   * the PD - 1 blocks requested after it. With loads under conditions it
+   * has to assume fewer and waited for nearly the whole ring. */
 #pragma unroll
-  for (int p = 0; p < PD; ++p)
-    if ((uint32_t)p < nblk) load_block((uint32_t)p, buf[p]);
+  for (int p = 0; p < PD; ++p) load_block((uint32_t)p, buf[p]);
 
   x_planes<MT>(nsc, xa, xb, xp, xf);
   __syncthreads();
@@ -310,7 +325,9 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const float d = F::dot(buf[u], cs + clc, xc);
-        acc[u][t] += (live && row0 + (uint32_t)(PAIR ? u / 2 : u) < r_end) ? d : 0.0f;
+        /* a bitwise select, not a branch around the dot product */
+        const uint32_t keep = (live && row0 + (uint32_t)(PAIR ? u / 2 : u) < r_end) ? ~0u : 0u;
+        acc[u][t] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, d) & keep);
       }
     }
     if (PAIR && s + 1u == steps) {
@@ -348,17 +365,23 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
     }
   };
 
-  for (uint32_t b0 = 0; b0 < nblk; b0 += (uint32_t)PD) {
+  /* Rounds of PD blocks: every round but the last refills each buffer
+   * right after its block (the refills of the round before the last may
+   * re-read the last block); the last round only computes, so no load is
+   * left to return before the wave retires. */
+  const uint32_t rounds = (nblk + (uint32_t)PD - 1u) / (uint32_t)PD;
+  uint32_t b0 = 0;
+  for (uint32_t rd = 1; rd < rounds; ++rd, b0 += (uint32_t)PD) {
 #pragma unroll
     for (int p = 0; p < PD; ++p) {
-      const uint32_t b = b0 + (uint32_t)p;
-      if (b < nblk) {
-        compute_block(b, buf[p]);
-        /* a refill past the wave's last block would still have to return
-         * before the wave can retire */
-        if (b + (uint32_t)PD < nblk) load_block(b + (uint32_t)PD, buf[p]);
-      }
+      compute_block(b0 + (uint32_t)p, buf[p]);
+      load_block(b0 + (uint32_t)p + (uint32_t)PD, buf[p]);
     }
+  }
+  if (rounds > 0u) {
+#pragma unroll
+    for (int p = 0; p < PD; ++p)
+      if (b0 + (uint32_t)p < nblk) compute_block(b0 + (uint32_t)p, buf[p]);
   }
 }
 

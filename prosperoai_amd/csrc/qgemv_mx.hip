@@ -282,12 +282,17 @@ __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, 
   for (int it = 0; it < XI; ++it) {
     const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
     const uint32_t ct = idx >> 2, t = ct / nch4, c = ct % nch4;
+    /* idle threads load nothing (a shared clamped address would make the
+     * L2 serve one line to every idle thread of every workgroup in turn) */
     const bool ok = ct < nct && t < ntok && c < nch;
-    const float4 *src =
-        reinterpret_cast<const float4 *>(x + (ok ? (size_t)t * k + 32u * c + 8u * (idx & 3u) : 0u));
-    const float4 a = src[0], b = src[1];
-    va[it] = make_float4(ok ? a.x : 0.f, ok ? a.y : 0.f, ok ? a.z : 0.f, ok ? a.w : 0.f);
-    vb[it] = make_float4(ok ? b.x : 0.f, ok ? b.y : 0.f, ok ? b.z : 0.f, ok ? b.w : 0.f);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (ok) {
+      const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)t * k + 32u * c + 8u * (idx & 3u));
+      a = src[0];
+      b = src[1];
+    }
+    va[it] = a;
+    vb[it] = b;
   }
 }
 
