@@ -387,6 +387,33 @@ def pmc_summary(fetch_csv: str, write_csv: str, copy_mib: int, kernel: str) -> d
             "traffic_bytes_per_launch": round(f_b * f_s + w_b * w_s)}
 
 
+def trace_summary(trace_csv: str, steps: int, warmup: int, layers: int) -> dict:
+    """Kernel durations of the headline's timed region from a rocprofv3
+    --kernel-trace CSV of a default run: the first Q4_0 GEMV dispatches are
+    the eager pass over the layers and the warm-up graph replays, then come
+    the timed steps (4 launches each, in step order qkv, o, gate_up, down)."""
+    import csv
+    rows = [r for r in csv.DictReader(open(trace_csv)) if "k_gemv<paik::Q4_0" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    nl = len(FUSED_STEP)
+    skip = nl * layers + nl * layers * max(1, -(-warmup // layers))
+    timed = rows[skip:skip + nl * steps]
+    if len(timed) != nl * steps:
+        raise RuntimeError(f"{trace_csv}: {len(rows)} Q4_0 GEMV dispatches, expected {skip} + {nl * steps}")
+    dur = np.array([int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in timed], float)
+    out = {"dispatches": len(timed), "skipped": skip,
+           "mean_ns": round(float(dur.mean()), 1),
+           "span_ns_per_launch": round((int(timed[-1]["End_Timestamp"]) -
+                                        int(timed[0]["Start_Timestamp"])) / len(timed), 1)}
+    for i, (name, _) in enumerate(FUSED_STEP):
+        d = dur[i::nl]
+        out[name] = {"kernel": timed[i]["Kernel_Name"], "grid": int(timed[i]["Grid_Size_X"]),
+                     "workgroup": int(timed[i]["Workgroup_Size_X"]),
+                     "mean_ns": round(float(d.mean()), 1), "median_ns": round(float(np.median(d)), 1),
+                     "min_ns": round(float(d.min()), 1)}
+    return out
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -410,10 +437,18 @@ def main() -> int:
                     help="skip the per-launch timings of the headline step")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with device copies of this size (counter calibration)")
+    ap.add_argument("--trace-summary", metavar="TRACE_CSV",
+                    help="summarise the headline's timed-region GEMV dispatches of a "
+                         "rocprofv3 --kernel-trace CSV of a run with the same --steps, "
+                         "--warmup and --layers, then exit")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "this script with --calib-copy-mib, then exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary, args.steps, args.warmup, args.layers),
+                         indent=1))
+        return 0
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.calib_copy_mib or 64,
                                      "k_gemv<paik::Q4_0")))
@@ -435,7 +470,7 @@ def main() -> int:
     avg_us = head["gpu_ms_per_step"] * 1e3 / head["launches_per_step"]
     roof = {"bound": "hbm", "achieved": round(head["gpu_GBps"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(head["gpu_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": "paik::k_gemv<paik::Q4_0, U, 1>",
+            "traffic": None, "kernel": "paik::k_gemv<paik::Q4_0, U, 1, false, NW>",
             "launches_per_step": head["launches_per_step"],
             "bytes_per_launch": round(head["bytes_per_step"] / head["launches_per_step"]),
             "avg_launch_us": round(avg_us, 3)}

@@ -186,14 +186,17 @@ pai_status_t pai_qmat_upload_gguf(pai_qmat_t **out, const pai_gguf_dir_t *d,
 
 /* flags for pai_qgemm_f32 / pai_qdequant_f32 */
 #define PAI_QGEMM_DEVICE_PTRS (1u << 0) /* x, y (out) are device pointers  */
-#define PAI_QGEMM_MFMA_BF16 (1u << 1)   /* M >= 8: bf16 MFMA operands       */
+#define PAI_QGEMM_MFMA_BF16 (1u << 1)   /* 16-bit MFMA path: bf16 operands  */
 #define PAI_QGEMM_FP32 (1u << 2)        /* any M: f32 dequant + f32 FMA path */
 
 /* y[m][n] = sum_k x[m][k] * W[n][k], x: [M][K] f32, y: [M][N] f32.
- *  - M < 8 (or PAI_QGEMM_FP32): blocks are multiplied with exact integer
- *    dot products against a 24-bit image of x and f32 accumulation.
- *    Matches the reference's sequential f32 sum within rel-L2 1e-5.
- *  - M >= 8: blocks are dequantized in registers to fp16 (default) or
+ *  - M < 8, M = 8 when K is a multiple of 128 up to 4096, or
+ *    PAI_QGEMM_FP32: blocks are multiplied with exact integer dot products
+ *    against a 24-bit image of x and f32 accumulation (one token on the
+ *    vector ALUs, 2 to 8 tokens per launch on the i8 matrix cores where K
+ *    is a multiple of 128). Matches the reference's sequential f32 sum
+ *    within rel-L2 1e-5.
+ *  - Otherwise (the 16-bit MFMA path): blocks are dequantized in registers to fp16 (default) or
  *    bf16, x is rounded to the same type, and MFMA accumulates in f32.
  *    Tolerance: rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16). Each matrix keeps
  *    a device workspace for a 16-bit copy of up to 1024 tokens of x,
@@ -217,11 +220,11 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
  * of one layer). All matrices must have the same type and K (otherwise
  * PAI_ERR_MISMATCH). x and every y_i are device pointers; `stream` is a
  * hipStream_t (NULL = the default stream); the call returns once the
- * kernels are enqueued. For M < 8 (or PAI_QGEMM_FP32) the matrices are
- * multiplied in one launch per group of up to 4 tokens, which streams all
+ * kernels are enqueued. On the integer-dot path (see pai_qgemm_f32) the
+ * matrices are multiplied in one launch per token group, which streams all
  * of their blocks and converts x once; results are bit-identical to
- * separate pai_qgemm_f32_async calls. For M >= 8 each matrix takes the
- * MFMA path of pai_qgemm_f32_async.
+ * separate pai_qgemm_f32_async calls. On the 16-bit MFMA path each matrix
+ * takes the MFMA path of pai_qgemm_f32_async.
  * No counterpart in the reference, whose executor runs each projection as
  * its own pai_ref_gemm_f32 (scheduler/scheduler.c:340); this is the fused
  * form of those calls for weights that share an input value
@@ -237,13 +240,13 @@ pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t cou
  * :484-488, :404-410); the gate and up products are never written out.
  * W_gate and W_up must have the same type, N and K (PAI_ERR_MISMATCH).
  * x and h are device pointers; `stream` as for pai_qgemm_f32_async.
- *  - M < 8 (or PAI_QGEMM_FP32): one launch per group of up to 4 tokens
- *    streams both matrices and applies the epilogue in registers; each
- *    token's gate and up sums are those pai_qgemm_f32_async computes for
- *    that token alone (M = 1), bit for bit, and silu uses the device expf
- *    (within 4 ulp of the reference's f32 composition applied to them).
- *    K up to 18720 (PAI_ERR_UNSUPPORTED above).
- *  - M >= 8: the gate product is written to h, then the up product's
+ *  - On the integer-dot path (see pai_qgemm_f32): one launch per token
+ *    group streams both matrices and applies the epilogue; the gate and up
+ *    sums are those pai_qgemm_f32_async computes for the same tokens, bit
+ *    for bit, and silu uses the device expf (within 4 ulp of the
+ *    reference's f32 composition applied to them). One token, or K not a
+ *    multiple of 128: K up to 18720 (PAI_ERR_UNSUPPORTED above).
+ *  - Otherwise: the gate product is written to h, then the up product's
  *    epilogue replaces each element by silu(h) * up (that launch is not
  *    split over K). Tolerances of the MFMA path. */
 pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate,
