@@ -25,6 +25,11 @@ ARCH = "gfx950"
 
 C_SOURCES = ["pai_hip.c", "pai_gguf.c", "paiq.c"]
 HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemv_mx.hip", "qgemm.hip"]
+# qgemm.hip is also compiled once per block format (object name, defines):
+# the four formats' GEMM kernels build in parallel
+HIP_VARIANTS = [(f"qgemm_{f.lower()}.hip", "qgemm.hip",
+                 [f"-DPAI_GEMM_FMT={f}", f"-DPAI_GEMM_ENTRY=paik_gemm_mfma_{f.lower()}"])
+                for f in ("Q4_K", "Q6_K", "Q4_0", "Q8_0")]
 HEADERS = ["paik.h", "qdev.h"]
 
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
@@ -43,22 +48,29 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {cmd[0]} ... {cmd[-1]}")
 
 
-def _compile(src: str) -> Path:
-    out = OBJ / (src + ".o")
+def _compile(item) -> Path:
+    """A C or HIP source, or (object name, HIP source, extra defines)."""
+    name, src, defs = item if isinstance(item, tuple) else (item, item, [])
+    out = OBJ / (name + ".o")
     if src.endswith(".c"):
         cmd = ["gcc", *C_FLAGS, "-c", str(CSRC / src), "-o", str(out)]
     else:
-        cmd = [HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(out)]
+        cmd = [HIPCC, *HIP_FLAGS, *defs, "-c", str(CSRC / src), "-o", str(out)]
     _run(cmd)
     return out
 
 
-def build_library(jobs: int = 4) -> Path:
+def units() -> list:
+    """Every compilation unit, longest first (so the pool starts them early)."""
+    return [*HIP_VARIANTS, "qgemv.hip", "qgemv_mx.hip", "qlayout.hip", "qgemm.hip", *C_SOURCES]
+
+
+def build_library(jobs: int = 6) -> Path:
     """Compile every source (always; this is also the 'does it build' check)."""
     OBJ.mkdir(parents=True, exist_ok=True)
     LIB.parent.mkdir(parents=True, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, C_SOURCES + HIP_SOURCES))
+        objs = list(ex.map(_compile, units()))
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp),
           *map(str, objs), "-lpthread", "-lm"])

@@ -482,6 +482,8 @@ __device__ __forceinline__ void wait_vmem() {
 
 /* x[m][k] f32 -> 16-bit copy (fp16 or bf16, round to nearest even), four
  * values per thread. */
+/* (templates only so that every per-format unit may hold a copy) */
+template <int = 0>
 __global__ void __launch_bounds__(256) k_cvt_x(const float4 *__restrict__ x,
                                                uint2 *__restrict__ out, size_t n4, int bf) {
   const size_t stride = (size_t)gridDim.x * 256u;
@@ -704,6 +706,7 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
 
 /* y[0 .. count) = 0 (a kernel, so that the call can be captured into a
  * graph). */
+template <int = 0>
 __global__ void __launch_bounds__(256) k_zero(float4 *__restrict__ y, size_t n4, float *tail,
                                               uint32_t ntail) {
   const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
@@ -716,11 +719,11 @@ static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
   const size_t pre = head < count ? head : count;
   const size_t n4 = (count - pre) / 4u, rest = count - pre - 4u * n4;
   /* the unaligned head and the tail: at most 6 floats, done by one thread each */
-  if (pre) k_zero<<<1, 256, 0, s>>>(nullptr, 0, y, (uint32_t)pre);
-  if (rest) k_zero<<<1, 256, 0, s>>>(nullptr, 0, y + pre + 4u * n4, (uint32_t)rest);
+  if (pre) k_zero<><<<1, 256, 0, s>>>(nullptr, 0, y, (uint32_t)pre);
+  if (rest) k_zero<><<<1, 256, 0, s>>>(nullptr, 0, y + pre + 4u * n4, (uint32_t)rest);
   if (n4) {
     const size_t blocks = (n4 + 255u) / 256u;
-    k_zero<<<dim3((unsigned)blocks), 256, 0, s>>>(reinterpret_cast<float4 *>(y + pre), n4,
+    k_zero<><<<dim3((unsigned)blocks), 256, 0, s>>>(reinterpret_cast<float4 *>(y + pre), n4,
                                                    nullptr, 0);
   }
   return hipGetLastError();
@@ -774,7 +777,7 @@ static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, 
                              float *y, const float *gate, bool bf16, hipStream_t s) {
   const size_t n4 = (size_t)m * v.k / 4u;
   const size_t blocks = (n4 + 255u) / 256u;
-  k_cvt_x<<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
+  k_cvt_x<><<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
       reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(x16), n4, bf16 ? 1 : 0);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -838,18 +841,29 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
 
 using namespace paik;
 
-extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
-                              const float *gate, int bf16, void *x16, uint64_t x16_bytes,
-                              void *stream) {
-  hipStream_t s = (hipStream_t)stream;
-  uint16_t *w16 = static_cast<uint16_t *>(x16);
-  const size_t wb = (size_t)x16_bytes;
-  const bool b = bf16 != 0;
+/* One translation unit per block format (PAI_GEMM_FMT = Q4_0, Q8_0, Q4_K or
+ * Q6_K, entry point PAI_GEMM_ENTRY), so the four formats' GEMM kernels
+ * compile in parallel; the unit without PAI_GEMM_FMT holds the dispatcher. */
+#define PAI_GEMM_ARGS                                                                         \
+  const paik_qview_t *v, uint32_t m, const float *x, float *y, const float *gate, int bf16,  \
+      void *x16, uint64_t x16_bytes, void *stream
+#ifdef PAI_GEMM_FMT
+extern "C" int PAI_GEMM_ENTRY(PAI_GEMM_ARGS) {
+  return (int)launch_gemm<PAI_GEMM_FMT>(*v, m, x, y, gate, bf16 != 0, static_cast<uint16_t *>(x16),
+                                        (size_t)x16_bytes, (hipStream_t)stream);
+}
+#else
+extern "C" int paik_gemm_mfma_q4_0(PAI_GEMM_ARGS);
+extern "C" int paik_gemm_mfma_q8_0(PAI_GEMM_ARGS);
+extern "C" int paik_gemm_mfma_q4_k(PAI_GEMM_ARGS);
+extern "C" int paik_gemm_mfma_q6_k(PAI_GEMM_ARGS);
+extern "C" int paik_gemm_mfma(PAI_GEMM_ARGS) {
   switch (v->type) {
-  case 8u: return (int)launch_gemm<Q8_0>(*v, m, x, y, gate, b, w16, wb, s);
-  case 2u: return (int)launch_gemm<Q4_0>(*v, m, x, y, gate, b, w16, wb, s);
-  case 12u: return (int)launch_gemm<Q4_K>(*v, m, x, y, gate, b, w16, wb, s);
-  case 14u: return (int)launch_gemm<Q6_K>(*v, m, x, y, gate, b, w16, wb, s);
+  case 8u: return paik_gemm_mfma_q8_0(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
+  case 2u: return paik_gemm_mfma_q4_0(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
+  case 12u: return paik_gemm_mfma_q4_k(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
+  case 14u: return paik_gemm_mfma_q6_k(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
   default: return (int)hipErrorInvalidValue;
   }
 }
+#endif

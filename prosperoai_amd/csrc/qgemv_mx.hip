@@ -52,6 +52,8 @@
  */
 #include <string.h>
 
+#include <type_traits>
+
 #include "qdev.h"
 
 namespace paik {
@@ -76,34 +78,40 @@ constexpr int xit() { return (int)(4u * kMaxChunkTok / (64u * (uint32_t)NW)); }
 template <class F, int MT>
 constexpr int ring() { return MT <= 2 && sizeof(typename F::Raw) <= 20 ? 8 : 6; }
 
-/* LDS layout: planes [MT][nch4][3][32] | zero [32] | scales [MT][nch4]
- * float4 {xs * f, sx0, sx1, sx0 + sx1} | partials [2][waves][MT][16]. */
+/* LDS layout: planes [MT][nch][3][32] | zero [32] | scales [MT][nch]
+ * float4 {xs * f, sx0, sx1, sx0 + sx1} | partials [2][waves][MT][rows per item]. */
 __host__ __device__ constexpr uint32_t lds_zero(uint32_t nct) { return nct * kPlaneBytes; }
 __host__ __device__ constexpr uint32_t lds_scales(uint32_t nct) { return lds_zero(nct) + 32u; }
 __host__ __device__ constexpr uint32_t lds_red(uint32_t nct) { return lds_scales(nct) + 16u * nct; }
-__host__ __device__ constexpr uint32_t lds_bytes(uint32_t nct, uint32_t mt, uint32_t nw) {
-  return lds_red(nct) + 2u * nw * mt * 16u * 4u;
+__host__ __device__ constexpr uint32_t lds_bytes(uint32_t nct, uint32_t mt, uint32_t nw,
+                                                  uint32_t ri) {
+  return lds_red(nct) + 2u * nw * mt * ri * 4u;
 }
 
-__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-/* sum of the three plane sums between two accumulator states,
- * D0 + 256 D1 + 65536 D2 */
-__device__ __forceinline__ float combine3(v4i c1, v4i c0) {
-  const int32_t p0 = c1.x - c0.x, p1 = c1.y - c0.y, p2 = c1.z - c0.z;
+/* One token's three plane sums over the first (a) and the second (b) MFMA
+ * of a step, exact integers. */
+struct Sums {
+  int32_t a0, a1, a2, b0, b1, b2;
+};
+/* D0 + 256 D1 + 65536 D2 of three plane sums, as f32 */
+__device__ __forceinline__ float combine3(int32_t p0, int32_t p1, int32_t p2) {
   return fmaf((float)p2, 65536.0f, (float)(p0 + (p1 << 8)));
+}
+__device__ __forceinline__ float comb_all(const Sums &s) {
+  return combine3(s.a0 + s.b0, s.a1 + s.b1, s.a2 + s.b2);
 }
 
 constexpr uint32_t kHi = 0xF0F0F0F0u, kLo = 0x0F0F0F0Fu;
 
 /* ------------------------------------------------------------------------
- * Formats. Each provides the lane-constant and item/step offsets of its
- * planes (lane, load), the weight operands of a step (bops), the lane's
- * chunk scale factors (ws) and one token's scale step (apply) from the
- * accumulator before, between and after the step's two MFMAs and the
- * token's chunk scale record sc = {xs * kXsScale, sx0, sx1, sx}.
+ * Formats. Each provides the lane-constant offsets of its planes (lane:
+ * row r, chunk slot g) and the loads of a step whose first chunk is cb
+ * (load), the weight operands of a step (bops), the scale factors of the
+ * lane's chunk c (ws) and one token's scale step (apply) from its exact
+ * plane sums over the step's two MFMAs and its chunk scale record
+ * sc = {xs * kXsScale, sx0, sx1, sx}.
  * ---------------------------------------------------------------------- */
 struct Offs {
   uint32_t q, aux, meta, d;
@@ -132,16 +140,16 @@ struct Q40 {
   __device__ static Offs lane(const QRes &R, uint32_t r, uint32_t g) {
     return {r * R.q_stride + 16u * g, 0u, 0u, 2u * (r * R.nb + g)};
   }
-  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t s) {
+  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t cb) {
     Raw w;
-    w.q = bl16(R.q, o.q, row0 * R.q_stride + 64u * s);
-    w.d = bl2(R.d, o.d, 2u * (row0 * R.nb + 4u * s));
+    w.q = bl16(R.q, o.q, row0 * R.q_stride + 16u * cb);
+    w.d = bl2(R.d, o.d, 2u * (row0 * R.nb + cb));
     return w;
   }
   __device__ static BOps bops(const Raw &w) { return nib16(w.q); }
-  __device__ static WS ws(const Raw &w, uint32_t, uint32_t) { return {h2f(w.d)}; }
-  __device__ static float apply(const WS &f, v4i c0, v4i, v4i c2, const float4 &sc) {
-    return (f.d * sc.x) * combine3(c2, c0);
+  __device__ static WS ws(const Raw &w, uint32_t) { return {h2f(w.d)}; }
+  __device__ static float apply(const WS &f, const Sums &s, const float4 &sc) {
+    return (f.d * sc.x) * comb_all(s);
   }
 };
 
@@ -159,22 +167,22 @@ struct Q4K {
   __device__ static Offs lane(const QRes &R, uint32_t r, uint32_t g) {
     return {r * R.q_stride + 16u * g, 0u, 16u * r * R.nb, 0u};
   }
-  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t s) {
+  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t cb) {
     Raw w;
-    w.q = bl16(R.q, o.q, row0 * R.q_stride + 64u * s);
-    w.m = bl16(R.meta, o.meta, 16u * (row0 * R.nb + (s >> 1)));
+    w.q = bl16(R.q, o.q, row0 * R.q_stride + 16u * cb);
+    w.m = bl16(R.meta, o.meta, 16u * (row0 * R.nb + (cb >> 3)));
     return w;
   }
   __device__ static BOps bops(const Raw &w) { return nib16(w.q); }
-  __device__ static WS ws(const Raw &w, uint32_t s, uint32_t g) {
+  __device__ static WS ws(const Raw &w, uint32_t c) {
     uint32_t s6, m6;
-    scale_min_k4(4u * (s & 1u) + g, w.m.y, w.m.z, w.m.w, s6, m6);
+    scale_min_k4(c & 7u, w.m.y, w.m.z, w.m.w, s6, m6);
     const float d1 = h2f_lo(w.m.x) * (float)s6;
     const float m1 = h2f_hi(w.m.x) * (float)m6;
     return {d1, fmaf(8.0f, d1, -m1)};
   }
-  __device__ static float apply(const WS &f, v4i c0, v4i, v4i c2, const float4 &sc) {
-    return fmaf(f.d1 * sc.x, combine3(c2, c0), f.b * sc.w);
+  __device__ static float apply(const WS &f, const Sums &s, const float4 &sc) {
+    return fmaf(f.d1 * sc.x, comb_all(s), f.b * sc.w);
   }
 };
 
@@ -194,12 +202,12 @@ struct Q6K {
   __device__ static Offs lane(const QRes &R, uint32_t r, uint32_t g) {
     return {r * R.q_stride + 16u * g, r * R.k4 + 8u * g, 16u * r * R.nb + 2u * g, 2u * r * R.nb};
   }
-  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t s) {
+  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t cb) {
     Raw w;
-    const uint32_t blk = row0 * R.nb + (s >> 1);
-    w.ql = bl16(R.q, o.q, row0 * R.q_stride + 64u * s);
-    w.qh = bl8(R.aux, o.aux, row0 * R.k4 + 32u * s);
-    w.sc = bl2(R.meta, o.meta, 16u * blk + 8u * (s & 1u));
+    const uint32_t blk = row0 * R.nb + (cb >> 3);
+    w.ql = bl16(R.q, o.q, row0 * R.q_stride + 16u * cb);
+    w.qh = bl8(R.aux, o.aux, row0 * R.k4 + 8u * cb);
+    w.sc = bl2(R.meta, o.meta, 16u * blk + 2u * (cb & 7u));
     w.d = bl2(R.d, o.d, 2u * blk);
     return w;
   }
@@ -217,13 +225,13 @@ struct Q6K {
     return {{code_lo(w.ql.x, h0), code_hi(w.ql.x, h0), code_lo(w.ql.y, h1), code_hi(w.ql.y, h1)},
             {code_lo(w.ql.z, h2), code_hi(w.ql.z, h2), code_lo(w.ql.w, h3), code_hi(w.ql.w, h3)}};
   }
-  __device__ static WS ws(const Raw &w, uint32_t, uint32_t) {
+  __device__ static WS ws(const Raw &w, uint32_t) {
     const float d = h2f(w.d);
     return {d * (float)(int32_t)(int8_t)(w.sc & 0xFFu), d * (float)(int32_t)(int8_t)(w.sc >> 8)};
   }
-  __device__ static float apply(const WS &f, v4i c0, v4i c1, v4i c2, const float4 &sc) {
-    const float t0 = fmaf(combine3(c1, c0), sc.x, -32.0f * sc.y);
-    const float t1 = fmaf(combine3(c2, c1), sc.x, -32.0f * sc.z);
+  __device__ static float apply(const WS &f, const Sums &s, const float4 &sc) {
+    const float t0 = fmaf(combine3(s.a0, s.a1, s.a2), sc.x, -32.0f * sc.y);
+    const float t1 = fmaf(combine3(s.b0, s.b1, s.b2), sc.x, -32.0f * sc.z);
     return fmaf(f.f0, t0, f.f1 * t1);
   }
 };
@@ -243,12 +251,12 @@ struct Q80 {
   __device__ static Offs lane(const QRes &R, uint32_t r, uint32_t g) {
     return {r * R.q_stride + 32u * g, 0u, 0u, 2u * (r * R.nb + g)};
   }
-  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t s) {
+  __device__ static Raw load(const QRes &R, const Offs &o, uint32_t row0, uint32_t cb) {
     Raw w;
-    const uint32_t so = row0 * R.q_stride + 128u * s;
+    const uint32_t so = row0 * R.q_stride + 32u * cb;
     w.lo = bl16(R.q, o.q, so);
     w.hi = bl16(R.q, o.q + 16u, so);
-    w.d = bl2(R.d, o.d, 2u * (row0 * R.nb + 4u * s));
+    w.d = bl2(R.d, o.d, 2u * (row0 * R.nb + cb));
     return w;
   }
   __device__ static int code_lo(uint32_t l, uint32_t h) {
@@ -263,9 +271,9 @@ struct Q80 {
             {code_lo(w.lo.z, w.hi.z), code_hi(w.lo.z, w.hi.z), code_lo(w.lo.w, w.hi.w),
              code_hi(w.lo.w, w.hi.w)}};
   }
-  __device__ static WS ws(const Raw &w, uint32_t, uint32_t) { return {h2f(w.d)}; }
-  __device__ static float apply(const WS &f, v4i c0, v4i, v4i c2, const float4 &sc) {
-    return (f.d * sc.x) * combine3(c2, c0);
+  __device__ static WS ws(const Raw &w, uint32_t) { return {h2f(w.d)}; }
+  __device__ static float apply(const WS &f, const Sums &s, const float4 &sc) {
+    return (f.d * sc.x) * comb_all(s);
   }
 };
 
@@ -367,8 +375,62 @@ __device__ __forceinline__ void x_planes(uint32_t nct, float xs_scale, const flo
 }
 
 /* ------------------------------------------------------------------------
- * The kernel.
+ * Tile shapes.
+ *   T16  v_mfma_i32_16x16x64_i8: items of 16 rows and steps of 4 chunks;
+ *        lane (r, g) = (l%16, l/16) loads chunk 4s + g of row r. One token
+ *        per pair of MFMAs: A row 4g + p holds plane p of the token's chunk
+ *        4s + g in k-set g (lanes 20g + p), and C lane (r, g) receives the
+ *        plane sums of its chunk in elements 0..2.
+ *   T32  v_mfma_i32_32x32x32_i8: items of 32 rows and steps of 2 chunks;
+ *        lane (r, g) = (l%32, l/32). Four tokens per pair of MFMAs: A row
+ *        8q + 4g + p holds plane p of token q's chunk 2s + g in k-set g
+ *        (lanes 8q + 36g + p), and C lane (r, g) receives token q's plane
+ *        sums of its chunk in elements 4q..4q+2. One A operand serves four
+ *        tokens, which cuts the activation reads from LDS fourfold.
  * ---------------------------------------------------------------------- */
+struct T16 {
+  static constexpr uint32_t RI = 16, CPS = 4, TPM = 1;
+  typedef v4i C;
+  __device__ static C mfma(v4i a, v4i b, C c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t row(uint32_t l) { return l & 15u; }
+  __device__ static uint32_t slot(uint32_t l) { return l >> 4; }
+  __device__ static bool a_lane(uint32_t l, uint32_t &q, uint32_t &g, uint32_t &p) {
+    q = 0u;
+    g = l / 20u;
+    p = l % 20u;
+    return p < 3u;
+  }
+  /* the chunk slots of a row: lanes r, r + 16, r + 32, r + 48 */
+  __device__ static float slot_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+  }
+};
+struct T32 {
+  static constexpr uint32_t RI = 32, CPS = 2, TPM = 4;
+  typedef v16i C;
+  __device__ static C mfma(v4i a, v4i b, C c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t row(uint32_t l) { return l & 31u; }
+  __device__ static uint32_t slot(uint32_t l) { return l >> 5; }
+  __device__ static bool a_lane(uint32_t l, uint32_t &q, uint32_t &g, uint32_t &p) {
+    g = l >= 36u ? 1u : 0u;
+    const uint32_t rem = l - 36u * g;
+    q = rem >> 3;
+    p = rem & 7u;
+    return p < 3u && q < 4u;
+  }
+  /* the chunk slots of a row: lanes r, r + 32 */
+  __device__ static float slot_sum(float v) { return v + __shfl_xor(v, 32, 64); }
+};
+
+/* the tile shape of a launch of MT tokens */
+template <int MT>
+using TileOf = typename std::conditional<(MT >= 4), T32, T16>::type;
+
 struct Args {
   paik_qview_t v[kMaxMats];
   float *y[kMaxMats];
@@ -381,13 +443,17 @@ template <class F, bool PAIR, int MT>
 __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const float *__restrict__ x,
                                                               uint32_t ntok) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  using T = TileOf<MT>;
   constexpr int R = ring<F, MT>();
   constexpr int NW = waves<MT>(), XI = xit<NW>();
+  constexpr uint32_t RI = T::RI, HALF = RI / 2u;
+  constexpr int NG = MT / (int)T::TPM; /* token groups, one accumulator each */
+  static_assert(MT % (int)T::TPM == 0, "whole token groups");
   const uint32_t k = a.v[0].k, nch = k >> 5;
-  const uint32_t nsteps = (nch + 3u) >> 2, nch4 = 4u * nsteps, nct = (uint32_t)MT * nch4;
+  const uint32_t nsteps = nch / T::CPS, nct = (uint32_t)MT * nch;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const uint32_t r = lane & 15u, g = lane >> 4;
+  const uint32_t r = T::row(lane), g = T::slot(lane);
 
   /* the workgroup's items and this wave's steps of each */
   const uint32_t i_beg = (uint32_t)((uint64_t)blockIdx.x * a.items / gridDim.x);
@@ -400,20 +466,22 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
   /* Load cursor: the item and step of the next load, with the buffer
    * resources of the item's matrix (or of gate and up) and the lane
    * offsets. Lanes of an item's rows past the matrix end read its last row
-   * (a paired item's lanes r and r + 8 read row r % 8 of gate and up), so
-   * every load stays inside the planes. */
+   * (a paired item's lanes r and r + RI/2 read row r % (RI/2) of gate and
+   * up), so every load stays inside the planes. Past the wave's last unit
+   * the cursor repeats the last item's steps (s_beg < nsteps for every
+   * wave), so every wave issues the same loads. */
   struct Cur {
     uint32_t it, s;
     QRes r0, r1;
     uint32_t row0;
     Offs o;
   } L;
-  const uint32_t rl = PAIR ? (r & 7u) : r;
+  const uint32_t rl = PAIR ? (r & (HALF - 1u)) : r;
   const Offs off_full = F::lane(make_qres(a.v[0]), rl, g); /* strides agree across matrices */
   auto item_of = [&](uint32_t it, uint32_t &mi, uint32_t &row0) {
     if constexpr (PAIR) {
       mi = 0u;
-      row0 = 8u * it;
+      row0 = HALF * it;
     } else {
       uint32_t base = 0u;
       mi = 0u;
@@ -423,7 +491,7 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
           mi = i;
           base = a.item_end[i - 1];
         }
-      row0 = 16u * (it - base);
+      row0 = RI * (it - base);
     }
   };
   auto enter = [&](uint32_t it) {
@@ -433,19 +501,21 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
     L.r0 = make_qres(a.v[mi]);
     if constexpr (PAIR) L.r1 = make_qres(a.v[1]);
     const uint32_t n = a.v[mi].n;
-    const uint32_t rows = PAIR ? 8u : 16u;
+    const uint32_t rows = PAIR ? HALF : RI;
     L.o = L.row0 + rows <= n ? off_full : F::lane(L.r0, min(rl, n - 1u - L.row0), g);
   };
   auto load_next = [&]() -> typename F::Raw {
     typename F::Raw w;
+    const uint32_t cb = T::CPS * L.s;
     if constexpr (PAIR) {
-      const typename F::Raw wg = F::load(L.r0, L.o, L.row0, L.s);
-      const typename F::Raw wu = F::load(L.r1, L.o, L.row0, L.s);
-      w = r < 8u ? wg : wu;
+      /* lanes of gate rows and of up rows load under complementary masks
+       * into the same registers */
+      if (r < HALF) w = F::load(L.r0, L.o, L.row0, cb);
+      else w = F::load(L.r1, L.o, L.row0, cb);
     } else {
-      w = F::load(L.r0, L.o, L.row0, L.s);
+      w = F::load(L.r0, L.o, L.row0, cb);
     }
-    if (++L.s == s_end) {
+    if (++L.s >= s_end) {
       L.s = s_beg;
       if (L.it + 1u < i_end) enter(L.it + 1u);
     }
@@ -461,57 +531,53 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
   enter(i_beg);
   {
     float4 xa[XI], xb[XI];
-    x_load(x, k, ntok, nch, nch4, nct, xa, xb);
+    x_load(x, k, ntok, nch, nch, nct, xa, xb);
     if constexpr (kEarlyRing) {
 #pragma unroll
-      for (int p = 0; p < R; ++p)
-        if ((uint32_t)p < nunits) buf[p] = load_next();
+      for (int p = 0; p < R; ++p) buf[p] = load_next();
     }
     if (threadIdx.x < 8u) reinterpret_cast<uint32_t *>(lds + lds_zero(nct))[threadIdx.x] = 0u;
     x_planes(nct, F::kXsScale, xa, xb, lds);
   }
   if constexpr (!kEarlyRing) {
 #pragma unroll
-    for (int p = 0; p < R; ++p)
-      if ((uint32_t)p < nunits) buf[p] = load_next();
+    for (int p = 0; p < R; ++p) buf[p] = load_next();
   }
   __syncthreads();
 
-  /* A operand addresses: lanes 20g + p (p < 3) read plane p of chunk
-   * 4s + g; the others read the zero block */
-  const uint32_t ag = lane / 20u, ap = lane % 20u;
-  const bool a_live = ap < 3u;
-  const uint32_t a_base = a_live ? (ag * 3u + ap) * 32u : lds_zero(nct);
-  const uint32_t a_step = a_live ? 4u * kPlaneBytes : 0u;
-  const uint32_t a_tok = a_live ? nch4 * kPlaneBytes : 0u;
+  /* A operand addresses: a carrying lane reads plane p of chunk
+   * CPS s + ga of token TPM gi + q; the others read the zero block */
+  uint32_t aq, ag, ap;
+  const bool a_live = T::a_lane(lane, aq, ag, ap);
+  const uint32_t a_base = a_live ? (aq * nch + ag) * kPlaneBytes + 32u * ap : lds_zero(nct);
+  const uint32_t a_step = a_live ? T::CPS * kPlaneBytes : 0u;
+  const uint32_t a_grp = a_live ? T::TPM * nch * kPlaneBytes : 0u;
   const float4 *scales = reinterpret_cast<const float4 *>(lds + lds_scales(nct));
   float *red = reinterpret_cast<float *>(lds + lds_red(nct));
 
   /* item end: the wave's partial sums of its rows into LDS slot it & 1, a
-   * barrier, then threads 0 .. 16 MT - 1 add the NW wave partials of one
+   * barrier, then threads 0 .. RI MT - 1 add the NW wave partials of one
    * (token, row) each and store the output */
   auto finish_item = [&](uint32_t it, const float (&acc)[MT]) {
-    float *slot = red + (it & 1u) * (uint32_t)(NW * MT * 16);
+    float *slot = red + (it & 1u) * (uint32_t)(NW * MT) * RI;
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      float v = acc[t];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (lane < 16u) slot[(wave * MT + (uint32_t)t) * 16u + lane] = v;
+      const float v = T::slot_sum(acc[t]);
+      if (lane < RI) slot[(wave * MT + (uint32_t)t) * RI + lane] = v;
     }
     __syncthreads();
     const uint32_t th = threadIdx.x;
-    if (th < 16u * MT) {
-      const uint32_t tt = th >> 4, rr = th & 15u;
+    if (th < RI * MT) {
+      const uint32_t tt = th / RI, rr = th % RI;
       float sum = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) sum += slot[((uint32_t)w * MT + tt) * 16u + rr];
+      for (int w = 0; w < NW; ++w) sum += slot[((uint32_t)w * MT + tt) * RI + rr];
       uint32_t mi, row0;
       item_of(it, mi, row0);
       if constexpr (PAIR) {
-        const float up = __shfl_down(sum, 8, 16); /* row rr + 8 of the item: the up sum */
+        const float up = __shfl_down(sum, HALF, RI); /* row rr + RI/2 of the item: the up sum */
         const uint32_t n = a.v[0].n, row = row0 + rr;
-        if (rr < 8u && row < n && tt < ntok) a.y[0][(size_t)tt * n + row] = silu_mul(sum, up);
+        if (rr < HALF && row < n && tt < ntok) a.y[0][(size_t)tt * n + row] = silu_mul(sum, up);
       } else {
         float *y = a.y[0];
 #pragma unroll
@@ -523,42 +589,60 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
     }
   };
 
-  v4i c[MT];
+  typename T::C c[NG];
   float acc[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    c[t] = v4i{0, 0, 0, 0};
-    acc[t] = 0.0f;
-  }
+  for (int q = 0; q < NG; ++q) c[q] = typename T::C{};
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
   uint32_t ci = i_beg, cs = s_beg; /* compute cursor */
-  for (uint32_t u0 = 0; u0 < nunits; u0 += (uint32_t)R) {
+  auto compute = [&](const typename F::Raw &w) {
+    const uint32_t cb = T::CPS * cs;
+    const BOps b = F::bops(w);
+    const typename F::WS f = F::ws(w, cb + g);
+    const uint8_t *ap_ = lds + a_base + a_step * cs;
 #pragma unroll
-    for (int p = 0; p < R; ++p) {
-      const uint32_t u = u0 + (uint32_t)p;
-      if (u < nunits) {
-        const BOps b = F::bops(buf[p]);
-        const typename F::WS f = F::ws(buf[p], cs, g);
-        const uint8_t *ap_ = lds + a_base + a_step * cs;
+    for (int q = 0; q < NG; ++q) {
+      const v4i a1 = *reinterpret_cast<const v4i *>(ap_ + a_grp * (uint32_t)q);
+      const v4i a2 = *reinterpret_cast<const v4i *>(ap_ + a_grp * (uint32_t)q + 16u);
+      const typename T::C c0 = c[q];
+      const typename T::C c1 = T::mfma(a1, b.b1, c0);
+      c[q] = T::mfma(a2, b.b2, c1);
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const v4i a1 = *reinterpret_cast<const v4i *>(ap_ + a_tok * (uint32_t)t);
-          const v4i a2 = *reinterpret_cast<const v4i *>(ap_ + a_tok * (uint32_t)t + 16u);
-          const float4 sc = scales[(uint32_t)t * nch4 + 4u * cs + g];
-          const v4i c0 = c[t];
-          const v4i c1 = mfma(a1, b.b1, c0);
-          c[t] = mfma(a2, b.b2, c1);
-          acc[t] += F::apply(f, c0, c1, c[t], sc);
-        }
-        if (u + (uint32_t)R < nunits) buf[p] = load_next();
-        if (++cs == s_end) {
-          finish_item(ci, acc);
-#pragma unroll
-          for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-          cs = s_beg;
-          ++ci;
-        }
+      for (int e = 0; e < (int)T::TPM; ++e) {
+        const int t = q * (int)T::TPM + e;
+        const Sums sm = {c1[4 * e] - c0[4 * e],     c1[4 * e + 1] - c0[4 * e + 1],
+                         c1[4 * e + 2] - c0[4 * e + 2], c[q][4 * e] - c1[4 * e],
+                         c[q][4 * e + 1] - c1[4 * e + 1], c[q][4 * e + 2] - c1[4 * e + 2]};
+        const float4 sc = scales[(uint32_t)t * nch + cb + g];
+        acc[t] += F::apply(f, sm, sc);
       }
     }
+    if (++cs == s_end) {
+      finish_item(ci, acc);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+      cs = s_beg;
+      ++ci;
+    }
+  };
+  /* Rounds of R steps: every round but the last refills each buffer right
+   * after its step, the last only computes. Every load is unconditional,
+   * so the compiler's wait before a step counts exactly the R - 1 steps
+   * requested after it. */
+  const uint32_t rounds = (nunits + (uint32_t)R - 1u) / (uint32_t)R;
+  uint32_t u0 = 0;
+  for (uint32_t rd = 1; rd < rounds; ++rd, u0 += (uint32_t)R) {
+#pragma unroll
+    for (int p = 0; p < R; ++p) {
+      compute(buf[p]);
+      buf[p] = load_next();
+    }
+  }
+  if (rounds > 0u) {
+#pragma unroll
+    for (int p = 0; p < R; ++p)
+      if (u0 + (uint32_t)p < nunits) compute(buf[p]);
   }
   if (spw == 0u) /* more waves than steps: zero partials, the same barriers */
     for (uint32_t i = i_beg; i < i_end; ++i) finish_item(i, acc);
@@ -566,10 +650,10 @@ __global__ void __launch_bounds__(64 * waves<MT>()) k_gemv_mx(Args a, const floa
 
 template <class F, bool PAIR, int MT>
 static hipError_t launch(const Args &a, const float *x, uint32_t ntok, hipStream_t s) {
-  const uint32_t nsteps = ((a.v[0].k >> 5) + 3u) >> 2;
+  const uint32_t nch = a.v[0].k >> 5;
   const uint32_t grid = a.items < 256u ? a.items : 256u;
   constexpr int NW = waves<MT>();
-  const size_t lds = lds_bytes((uint32_t)MT * 4u * nsteps, (uint32_t)MT, (uint32_t)NW);
+  const size_t lds = lds_bytes((uint32_t)MT * nch, (uint32_t)MT, (uint32_t)NW, TileOf<MT>::RI);
   k_gemv_mx<F, PAIR, MT><<<dim3(grid), dim3(64u * NW), lds, s>>>(a, x, ntok);
   return hipGetLastError();
 }
@@ -616,12 +700,13 @@ static size_t lds_max() {
  * even one token does not fit. */
 static uint32_t tokens_for(uint32_t k, uint32_t m) {
   if ((k & 127u) != 0u || k == 0u) return 0u;
-  const uint32_t nch4 = k >> 5;
+  const uint32_t nch = k >> 5;
   uint32_t mt = 1u;
   while (mt < m && mt < 8u) mt <<= 1;
-  for (; mt >= 1u; mt >>= 1)
-    if (mt * nch4 <= kMaxChunkTok && lds_bytes(mt * nch4, mt, mt <= 2u ? 16u : 8u) <= lds_max())
-      return mt;
+  for (; mt >= 1u; mt >>= 1) {
+    const uint32_t nw = mt <= 2u ? 16u : 8u, ri = mt >= 4u ? 32u : 16u;
+    if (mt * nch <= kMaxChunkTok && lds_bytes(mt * nch, mt, nw, ri) <= lds_max()) return mt;
+  }
   return 0u;
 }
 
@@ -636,13 +721,14 @@ extern "C" int paik_gemv_mx(const paik_qview_t *const *vs, float *const *ys, uin
                             uint32_t m, const float *x, void *stream) {
   const uint32_t mt = mx::tokens_for(vs[0]->k, m);
   if (count == 0u || count > mx::kMaxMats || mt == 0u || m == 0u) return (int)hipErrorInvalidValue;
+  const uint32_t ri = mt >= 4u ? 32u : 16u;
   mx::Args a;
   memset(&a, 0, sizeof a);
   a.count = count;
   uint32_t items = 0;
   for (uint32_t i = 0; i < count; ++i) {
     a.v[i] = *vs[i];
-    items += (vs[i]->n + 15u) >> 4;
+    items += (vs[i]->n + ri - 1u) / ri;
     a.item_end[i] = items;
   }
   a.items = items;
@@ -660,12 +746,13 @@ extern "C" int paik_gemv_mx_silu_mul(const paik_qview_t *gate, const paik_qview_
                                      const float *x, float *h, void *stream) {
   const uint32_t mt = mx::tokens_for(gate->k, m);
   if (mt == 0u || m == 0u) return (int)hipErrorInvalidValue;
+  const uint32_t half = mt >= 4u ? 16u : 8u;
   mx::Args a;
   memset(&a, 0, sizeof a);
   a.count = 2;
   a.v[0] = *gate;
   a.v[1] = *up;
-  a.items = (gate->n + 7u) >> 3;
+  a.items = (gate->n + half - 1u) / half;
   a.item_end[0] = a.items;
   for (uint32_t t0 = 0; t0 < m; t0 += mt) {
     a.y[0] = h + (size_t)t0 * gate->n;
