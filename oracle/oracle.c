@@ -580,3 +580,262 @@ void orc_q4_0_encode_ref(const float *x, uint8_t *out, uint64_t numel) {
     }
   }
 }
+
+/* ---------------------------------------------------------------------- */
+/* Decode step of the LLaMA graph                                           */
+/* ---------------------------------------------------------------------- */
+
+uint16_t orc_f32_to_f16(float v) { return f32_to_f16_rne(v); }
+
+/* c = a * gamma * rms, rms = 1 / sqrtf((float)(sum a^2 / n) + eps), the
+ * sum sequential in double; eps == 0 means 1e-5.
+ * Follows cpu/reference/ref_ops.c:196-218. */
+int32_t orc_rmsnorm_gamma_f32(const float *a, float *c, uint64_t n, const float *gamma,
+                              float eps) {
+  if (n == 0u || a == NULL || c == NULL || gamma == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  if (eps == 0.0f) {
+    eps = 1e-5f;
+  }
+  double acc = 0.0;
+  for (uint64_t i = 0; i < n; ++i) {
+    acc += (double)a[i] * (double)a[i];
+  }
+  const float rms = 1.0f / sqrtf((float)(acc / (double)n) + eps);
+  for (uint64_t i = 0; i < n; ++i) {
+    c[i] = a[i] * gamma[i] * rms;
+  }
+  return ORC_OK;
+}
+
+/* Rotary embedding of `rows` rows of hd floats, position-major
+ * (row = p * heads + h): pairs (i, i + r2) of position p's row rotated by
+ * cos_t/sin_t[p * r2 + i]; columns from 2 r2 on are copied.
+ * Follows cpu/reference/ref_ops.c:231-256. */
+int32_t orc_rope_f32(const float *x, uint64_t rows, uint64_t hd, uint64_t seq, uint64_t heads,
+                     const float *cos_t, const float *sin_t, uint64_t r2, float *out) {
+  if (rows == 0u || hd == 0u || seq == 0u || heads == 0u || r2 == 0u || 2u * r2 > hd ||
+      rows % heads != 0u || x == NULL || out == NULL || cos_t == NULL || sin_t == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  for (uint64_t row = 0; row < rows; ++row) {
+    const uint64_t p = row / heads;
+    const float *xr = x + row * hd;
+    float *o = out + row * hd;
+    for (uint64_t i = 0; i < r2; ++i) {
+      const float c = cos_t[p * r2 + i], s = sin_t[p * r2 + i];
+      const float x0 = xr[i], x1 = xr[i + r2];
+      o[i] = x0 * c - x1 * s;
+      o[i + r2] = x0 * s + x1 * c;
+    }
+    for (uint64_t i = 2u * r2; i < hd; ++i) {
+      o[i] = xr[i];
+    }
+  }
+  return ORC_OK;
+}
+
+/* The adapter's RoPE tables for positions 0..ctx-1:
+ * freq_i = powf(theta, -(float)(2 i) / (float)n_rot),
+ * cos_t[p][i] = cosf((float)p * freq_i), sin_t[p][i] = sinf(...).
+ * Follows adapters/llama/llama.c:855-861. */
+void orc_rope_tables_llama(uint32_t ctx, uint32_t r2, uint32_t n_rot, float theta, float *cos_t,
+                           float *sin_t) {
+  for (uint32_t p = 0; p < ctx; ++p) {
+    for (uint32_t i = 0; i < r2; ++i) {
+      const float freq = powf(theta, -(float)(2u * i) / (float)n_rot);
+      cos_t[(uint64_t)p * r2 + i] = cosf((float)p * freq);
+      sin_t[(uint64_t)p * r2 + i] = sinf((float)p * freq);
+    }
+  }
+}
+
+/* One (query, head) row of causal attention over keys/values 0..p, each
+ * key/value row given by a pointer function of its position. */
+static void attention_row(const float *qp, uint64_t p, uint64_t hd, float inv_scale,
+                          const float *kbase, const float *vbase, uint64_t stride, float *scores,
+                          float *op) {
+  for (uint64_t i = 0; i <= p; ++i) {
+    const float *kp = kbase + i * stride;
+    float dot = 0.0f;
+    for (uint64_t d = 0; d < hd; ++d) {
+      dot += qp[d] * kp[d];
+    }
+    scores[i] = dot * inv_scale;
+  }
+  float maxv = scores[0];
+  for (uint64_t i = 1; i <= p; ++i) {
+    if (scores[i] > maxv) {
+      maxv = scores[i];
+    }
+  }
+  float sum = 0.0f;
+  for (uint64_t i = 0; i <= p; ++i) {
+    const float e = expf(scores[i] - maxv);
+    scores[i] = e;
+    sum += e;
+  }
+  for (uint64_t i = 0; i <= p; ++i) {
+    scores[i] /= sum;
+  }
+  for (uint64_t d = 0; d < hd; ++d) {
+    float acc = 0.0f;
+    for (uint64_t i = 0; i <= p; ++i) {
+      acc += scores[i] * vbase[i * stride + d];
+    }
+    op[d] = acc;
+  }
+}
+
+/* Causal multi-head attention, position-major buffers: q, out [seq][h][hd],
+ * k, v [seq][hk][hd]; head hh reads KV head (hh * hk) / h.
+ * Follows cpu/reference/ref_ops.c:287-350. */
+int32_t orc_attention_f32(uint64_t h, uint64_t hk, uint64_t seq, uint64_t hd, const float *q,
+                          const float *k, const float *v, float *out) {
+  if (h == 0u || hk == 0u || seq == 0u || hd == 0u || h % hk != 0u || q == NULL || k == NULL ||
+      v == NULL || out == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  float *scores = (float *)malloc((size_t)seq * sizeof(float));
+  if (scores == NULL) {
+    return ORC_ERR_NOMEM;
+  }
+  const float inv_scale = 1.0f / sqrtf((float)hd);
+  for (uint64_t p = 0; p < seq; ++p) {
+    for (uint64_t hh = 0; hh < h; ++hh) {
+      const uint64_t kvh = (hh * hk) / h;
+      attention_row(q + (p * h + hh) * hd, p, hd, inv_scale, k + kvh * hd, v + kvh * hd, hk * hd,
+                    scores, out + (p * h + hh) * hd);
+    }
+  }
+  free(scores);
+  return ORC_OK;
+}
+
+/* The last row (position len - 1) of orc_attention_f32, with keys and
+ * values read from caches laid out [hk][ctx][hd]. q, out: [h][hd]. */
+int32_t orc_attention_last_f32(uint64_t h, uint64_t hk, uint64_t ctx, uint64_t len, uint64_t hd,
+                               const float *q, const float *k_cache, const float *v_cache,
+                               float *out) {
+  if (h == 0u || hk == 0u || len == 0u || len > ctx || hd == 0u || h % hk != 0u || q == NULL ||
+      k_cache == NULL || v_cache == NULL || out == NULL) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  float *scores = (float *)malloc((size_t)len * sizeof(float));
+  if (scores == NULL) {
+    return ORC_ERR_NOMEM;
+  }
+  const float inv_scale = 1.0f / sqrtf((float)hd);
+  for (uint64_t hh = 0; hh < h; ++hh) {
+    const uint64_t kvh = (hh * hk) / h;
+    attention_row(q + hh * hd, len - 1u, hd, inv_scale, k_cache + kvh * ctx * hd,
+                  v_cache + kvh * ctx * hd, hd, scores, out + hh * hd);
+  }
+  free(scores);
+  return ORC_OK;
+}
+
+/* Greedy pick: best = x[0], then i replaces it when x[i] > best.
+ * Follows models/sampler.c:146-155. */
+uint32_t orc_argmax_first(const float *x, uint64_t n) {
+  float best = x[0];
+  uint32_t chosen = 0;
+  for (uint64_t i = 1; i < n; ++i) {
+    if (x[i] > best) {
+      best = x[i];
+      chosen = (uint32_t)i;
+    }
+  }
+  return chosen;
+}
+
+/* y[j] = sum_l x[l] * w[j][l], sequential f32: pai_ref_gemm_f32
+ * (cpu/reference/ref_ops.c:427-444) on the transposed weight
+ * (adapters/llama/llama.c:196-209) for one row of activations. */
+static void gemv_seq(const float *w, uint64_t n, uint64_t k, const float *x, float *y) {
+  for (uint64_t j = 0; j < n; ++j) {
+    float acc = 0.0f;
+    for (uint64_t l = 0; l < k; ++l) {
+      acc += x[l] * w[j * k + l];
+    }
+    y[j] = acc;
+  }
+}
+
+/* One decode position of the adapter's graph (adapters/llama/llama.c:
+ * 499-800, the last row of a sequence-mode run, models/model.c:453-507),
+ * with the keys and values of earlier positions read from m's caches and
+ * this position's appended to them (rounded to fp16 when m->kv_f16). */
+int32_t orc_llama_step(const orc_llama_t *m, uint32_t token, uint32_t pos, float *logits,
+                       uint32_t *next) {
+  if (m == NULL || logits == NULL || next == NULL || token >= m->vocab || pos >= m->ctx ||
+      m->n_head == 0u || m->n_head_kv == 0u || m->n_embd % m->n_head != 0u) {
+    return ORC_ERR_INVALID_ARG;
+  }
+  const uint64_t E = m->n_embd, F = m->n_ff, H = m->n_head, HK = m->n_head_kv;
+  const uint64_t hd = E / H, kvd = HK * hd;
+  uint32_t n_rot = m->n_rot;
+  if (n_rot == 0u || n_rot > hd || (n_rot & 1u) != 0u) {
+    n_rot = (uint32_t)hd; /* adapters/llama/llama.c:372-375 */
+  }
+  const uint32_t r2 = n_rot / 2u;
+  const float theta = m->rope_theta != 0.0f ? m->rope_theta : 10000.0f;
+  const uint64_t nf = 5u * E + 3u * E + 2u * kvd + 3u * F + 2u * r2;
+  float *buf = (float *)malloc(nf * sizeof(float));
+  float *cs = (float *)malloc((size_t)(pos + 1u) * r2 * 2u * sizeof(float));
+  if (buf == NULL || cs == NULL) {
+    free(buf);
+    free(cs);
+    return ORC_ERR_NOMEM;
+  }
+  float *x = buf, *xn = x + E, *o = xn + E, *t = o + E, *a = t + E, *q = a + E, *qr = q + E;
+  float *kr = qr + E, *k = kr + E, *v = k + kvd, *g = v + kvd, *u = g + F, *hh = u + F;
+  float *cos_t = cs, *sin_t = cs + (size_t)(pos + 1u) * r2;
+  orc_rope_tables_llama(pos + 1u, r2, n_rot, theta, cos_t, sin_t);
+  /* the rope ops of this position read the tables at row pos */
+  const float *cp = cos_t + (size_t)pos * r2, *sp = sin_t + (size_t)pos * r2;
+
+  memcpy(x, m->token_embd + (size_t)token * E, E * sizeof(float)); /* one-hot GEMM */
+  for (uint32_t l = 0; l < m->n_layer; ++l) {
+    const float *const *w = m->w + (size_t)l * 7u;
+    orc_rmsnorm_gamma_f32(x, xn, E, m->attn_norm + (size_t)l * E, m->norm_eps);
+    gemv_seq(w[0], E, E, xn, q);
+    gemv_seq(w[1], kvd, E, xn, k);
+    gemv_seq(w[2], kvd, E, xn, v);
+    orc_rope_f32(q, H, hd, 1u, H, cp, sp, r2, qr);
+    orc_rope_f32(k, HK, hd, 1u, HK, cp, sp, r2, kr);
+    float *kc = m->k_cache + (size_t)l * HK * m->ctx * hd;
+    float *vc = m->v_cache + (size_t)l * HK * m->ctx * hd;
+    for (uint64_t h = 0; h < HK; ++h) {
+      for (uint64_t d = 0; d < hd; ++d) {
+        float kv = kr[h * hd + d], vv = v[h * hd + d];
+        if (m->kv_f16) {
+          kv = orc_f16_to_f32(f32_to_f16_rne(kv));
+          vv = orc_f16_to_f32(f32_to_f16_rne(vv));
+        }
+        kc[(h * m->ctx + pos) * hd + d] = kv;
+        vc[(h * m->ctx + pos) * hd + d] = vv;
+      }
+    }
+    orc_attention_last_f32(H, HK, m->ctx, pos + 1u, hd, qr, kc, vc, a);
+    gemv_seq(w[3], E, E, a, o);
+    for (uint64_t i = 0; i < E; ++i) {
+      x[i] = x[i] + o[i]; /* pai_ref_vecadd_f32 */
+    }
+    orc_rmsnorm_gamma_f32(x, xn, E, m->ffn_norm + (size_t)l * E, m->norm_eps);
+    gemv_seq(w[4], F, E, xn, g);
+    gemv_seq(w[5], F, E, xn, u);
+    orc_silu_mul_f32(g, u, hh, F);
+    gemv_seq(w[6], E, F, hh, t);
+    for (uint64_t i = 0; i < E; ++i) {
+      x[i] = x[i] + t[i];
+    }
+  }
+  orc_rmsnorm_gamma_f32(x, xn, E, m->output_norm, m->norm_eps);
+  gemv_seq(m->output, m->vocab, E, xn, logits);
+  *next = orc_argmax_first(logits, m->vocab);
+  free(buf);
+  free(cs);
+  return ORC_OK;
+}

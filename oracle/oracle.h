@@ -31,6 +31,24 @@
  *                         (silu(0) = 0, silu(x) -> x, silu(-x) -> -0).
  *   orc_opt_gemv_avx2 /   the reference's opt_ops.c built into oracle/_ref
  *   orc_opt_gemm_w8_avx2  (bit-exact), and tolerance vs the f64 oracle.
+ *   orc_rmsnorm_gamma_f32 the reference's ref_ops.c built into oracle/_ref
+ *   orc_rope_f32          (bit-exact), plus closed forms: a constant row
+ *   orc_attention_f32     normalises to gamma / sqrt(1 + eps/c^2); RoPE at
+ *                         position 0 is the identity and preserves pair
+ *                         norms; attention over one position returns v,
+ *                         over equal keys the mean of v.
+ *   orc_attention_last_f32 equals the last row of orc_attention_f32 on
+ *                         the same keys and values (bit-exact).
+ *   orc_rope_tables_llama f64 closed form cos(p theta^(-2i/n_rot)).
+ *   orc_argmax_first      numpy's first-occurrence argmax on NaN-free rows,
+ *                         and hand cases for ties and NaNs.
+ *   orc_f32_to_f16        numpy float32 -> float16 (round to nearest even)
+ *                         on special values and random bit patterns.
+ *   orc_llama_step        composition of the above with the sequential
+ *                         GEMM; with kv_f16 = 0 and a prompt run token by
+ *                         token it equals the reference's sequence-mode
+ *                         graph restated with orc_attention_f32 over all
+ *                         positions (last row, bit-exact).
  *   orc_q8_0_encode_ref / textbook llama.cpp encoders used to pin the
  *   orc_q4_0_encode_ref   product encoders; the reference has no encoder,
  *                         so these two are pinned only by round-trip
@@ -90,6 +108,36 @@ int32_t orc_opt_gemm_w8_avx2(uint64_t m, uint64_t n, uint64_t k,
 
 void orc_q8_0_encode_ref(const float *x, uint8_t *out, uint64_t numel);
 void orc_q4_0_encode_ref(const float *x, uint8_t *out, uint64_t numel);
+
+/* Decode step of the LLaMA graph (adapters/llama/llama.c). */
+uint16_t orc_f32_to_f16(float v);
+int32_t orc_rmsnorm_gamma_f32(const float *a, float *c, uint64_t n, const float *gamma,
+                              float eps);
+int32_t orc_rope_f32(const float *x, uint64_t rows, uint64_t hd, uint64_t seq, uint64_t heads,
+                     const float *cos_t, const float *sin_t, uint64_t r2, float *out);
+void orc_rope_tables_llama(uint32_t ctx, uint32_t r2, uint32_t n_rot, float theta, float *cos_t,
+                           float *sin_t);
+int32_t orc_attention_f32(uint64_t h, uint64_t hk, uint64_t seq, uint64_t hd, const float *q,
+                          const float *k, const float *v, float *out);
+int32_t orc_attention_last_f32(uint64_t h, uint64_t hk, uint64_t ctx, uint64_t len, uint64_t hd,
+                               const float *q, const float *k_cache, const float *v_cache,
+                               float *out);
+uint32_t orc_argmax_first(const float *x, uint64_t n);
+
+/* A model for orc_llama_step: dequantized weights W[N][K] (row-major f32)
+ * and f32 caches [n_layer][n_head_kv][ctx][hd], all owned by the caller. */
+typedef struct orc_llama {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, vocab, ctx, n_rot;
+  float rope_theta, norm_eps;
+  const float *const *w; /* [n_layer * 7]: q, k, v, o, gate, up, down */
+  const float *attn_norm, *ffn_norm; /* [n_layer][n_embd] */
+  const float *token_embd, *output;  /* [vocab][n_embd] */
+  const float *output_norm;          /* [n_embd] */
+  float *k_cache, *v_cache;
+  int32_t kv_f16; /* round appended keys and values to fp16 */
+} orc_llama_t;
+int32_t orc_llama_step(const orc_llama_t *m, uint32_t token, uint32_t pos, float *logits,
+                       uint32_t *next);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,14 @@ _ORACLE_SIGS = {
     "orc_opt_gemm_w8_avx2": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
     "orc_q8_0_encode_ref": (None, [_vp, _vp, C.c_uint64]),
     "orc_q4_0_encode_ref": (None, [_vp, _vp, C.c_uint64]),
+    "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+    "orc_rmsnorm_gamma_f32": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, C.c_float]),
+    "orc_rope_f32": (C.c_int32, [_vp] + [C.c_uint64] * 4 + [_vp, _vp, C.c_uint64, _vp]),
+    "orc_rope_tables_llama": (None, [C.c_uint32] * 3 + [C.c_float, _vp, _vp]),
+    "orc_attention_f32": (C.c_int32, [C.c_uint64] * 4 + [_vp] * 4),
+    "orc_attention_last_f32": (C.c_int32, [C.c_uint64] * 5 + [_vp] * 4),
+    "orc_argmax_first": (C.c_uint32, [_vp, C.c_uint64]),
+    "orc_llama_step": (C.c_int32, [_vp, C.c_uint32, C.c_uint32, _vp, _vp]),
 }
 
 _REF_SIGS = {
@@ -48,6 +56,10 @@ _REF_SIGS = {
     "pai_ref_gemm_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
     "pai_ref_silu_f32": (C.c_int32, [_vp, _vp, C.c_uint64]),
     "pai_ref_vecmul_f32": (C.c_int32, [_vp, _vp, _vp, C.c_uint64]),
+    "pai_ref_vecadd_f32": (C.c_int32, [_vp, _vp, _vp, C.c_uint64]),
+    "pai_ref_rmsnorm_gamma_f32": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, C.c_float]),
+    "pai_ref_rope_f32": (C.c_int32, [_vp] + [C.c_uint64] * 4 + [_vp, _vp, C.c_uint64, _vp]),
+    "pai_ref_attention_f32": (C.c_int32, [C.c_uint64] * 4 + [_vp] * 4),
     "pai_opt_gemv_f32": (C.c_int32, [C.c_uint64, C.c_uint64, _vp, _vp, _vp]),
     "pai_opt_gemm_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
     "pai_opt_gemm_w8_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
@@ -141,6 +153,121 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     if st != 0:
         raise RuntimeError(f"orc_silu_mul_f32 status {st}")
     return h
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _check(st: int, name: str) -> None:
+    if st != 0:
+        raise RuntimeError(f"{name} status {st}")
+
+
+def f32_to_f16(v: np.ndarray) -> np.ndarray:
+    """orc_f32_to_f16 on every element (binary16 bit patterns)."""
+    o = oracle()
+    return np.array([o.orc_f32_to_f16(float(x)) for x in _f32(v).ravel()], np.uint16)
+
+
+def rmsnorm(a: np.ndarray, gamma: np.ndarray, eps: float = 0.0) -> np.ndarray:
+    a, gamma = _f32(a), _f32(gamma)
+    c = np.empty_like(a)
+    _check(oracle().orc_rmsnorm_gamma_f32(_p(a), _p(c), a.size, _p(gamma), eps), "rmsnorm")
+    return c
+
+
+def rope(x: np.ndarray, heads: int, cos_t: np.ndarray, sin_t: np.ndarray, r2: int) -> np.ndarray:
+    """x: [seq * heads][hd] position-major; tables [seq][r2]."""
+    x, cos_t, sin_t = _f32(x), _f32(cos_t), _f32(sin_t)
+    rows, hd = x.shape
+    out = np.empty_like(x)
+    _check(oracle().orc_rope_f32(_p(x), rows, hd, rows // heads, heads, _p(cos_t), _p(sin_t), r2,
+                                 _p(out)), "rope")
+    return out
+
+
+def rope_tables(ctx: int, r2: int, n_rot: int, theta: float):
+    c = np.empty((ctx, r2), np.float32)
+    s = np.empty((ctx, r2), np.float32)
+    oracle().orc_rope_tables_llama(ctx, r2, n_rot, theta, _p(c), _p(s))
+    return c, s
+
+
+def attention(h: int, hk: int, q: np.ndarray, k: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """q: [seq][h][hd], k, v: [seq][hk][hd] -> [seq][h][hd] (causal)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    seq, hd = q.shape[0], q.shape[-1]
+    out = np.empty_like(q)
+    _check(oracle().orc_attention_f32(h, hk, seq, hd, _p(q), _p(k), _p(v), _p(out)), "attention")
+    return out
+
+
+def attention_last(h: int, hk: int, length: int, q: np.ndarray, kc: np.ndarray,
+                   vc: np.ndarray) -> np.ndarray:
+    """q: [h][hd]; caches [hk][ctx][hd] -> [h][hd] over positions < length."""
+    q, kc, vc = _f32(q), _f32(kc), _f32(vc)
+    ctx, hd = kc.shape[1], kc.shape[2]
+    out = np.empty((h, hd), np.float32)
+    _check(oracle().orc_attention_last_f32(h, hk, ctx, length, hd, _p(q), _p(kc), _p(vc),
+                                           _p(out)), "attention_last")
+    return out
+
+
+def argmax_first(x: np.ndarray) -> int:
+    x = _f32(x)
+    return int(oracle().orc_argmax_first(_p(x), x.size))
+
+
+class _OrcLlama(C.Structure):
+    """orc_llama_t (oracle/oracle.h)."""
+    _fields_ = [(n, C.c_uint32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "n_ff",
+                                          "vocab", "ctx", "n_rot")] + [
+        ("rope_theta", C.c_float), ("norm_eps", C.c_float), ("w", C.POINTER(C.c_void_p)),
+        ("attn_norm", _vp), ("ffn_norm", _vp), ("token_embd", _vp), ("output", _vp),
+        ("output_norm", _vp), ("k_cache", _vp), ("v_cache", _vp), ("kv_f16", C.c_int32)]
+
+
+class LlamaOracle:
+    """orc_llama_step over dequantized weights.
+
+    cfg: dict with n_layer, n_embd, n_head, n_head_kv, n_ff, vocab, ctx,
+    n_rot, rope_theta, norm_eps. layers: list of dicts with f32 matrices
+    q, k, v, o, gate, up, down ([N][K]) and attn_norm, ffn_norm; head: dict
+    with token_embd, output ([vocab][n_embd]) and output_norm."""
+
+    def __init__(self, cfg: dict, layers: list, head: dict, kv_f16: bool = True):
+        self.cfg = cfg
+        hd = cfg["n_embd"] // cfg["n_head"]
+        self._keep = []
+        ws = []
+        for L in layers:
+            for name in ("q", "k", "v", "o", "gate", "up", "down"):
+                a = _f32(L[name])
+                self._keep.append(a)
+                ws.append(_p(a))
+        self._w = (C.c_void_p * len(ws))(*ws)
+        self.attn_norm = _f32(np.stack([L["attn_norm"] for L in layers]))
+        self.ffn_norm = _f32(np.stack([L["ffn_norm"] for L in layers]))
+        self.token_embd = _f32(head["token_embd"])
+        self.output = _f32(head["output"])
+        self.output_norm = _f32(head["output_norm"])
+        shape = (cfg["n_layer"], cfg["n_head_kv"], cfg["ctx"], hd)
+        self.k_cache = np.zeros(shape, np.float32)
+        self.v_cache = np.zeros(shape, np.float32)
+        self._m = _OrcLlama(
+            *[cfg[n] for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "n_ff", "vocab", "ctx",
+                               "n_rot")],
+            cfg["rope_theta"], cfg["norm_eps"], self._w, _p(self.attn_norm), _p(self.ffn_norm),
+            _p(self.token_embd), _p(self.output), _p(self.output_norm), _p(self.k_cache),
+            _p(self.v_cache), 1 if kv_f16 else 0)
+
+    def step(self, token: int, pos: int):
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        nxt = C.c_uint32()
+        _check(oracle().orc_llama_step(C.byref(self._m), token, pos, _p(logits), C.byref(nxt)),
+               "orc_llama_step")
+        return logits, nxt.value
 
 
 # ---------------------------------------------------------------- reference wrappers

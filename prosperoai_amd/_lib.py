@@ -53,6 +53,23 @@ SIGNATURES = {
     "pai_qmat_upload_gguf": (C.c_int32, [C.POINTER(C.c_void_p), _vp, C.c_char_p]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),
     "pai_hip_op_name": (C.c_char_p, [C.c_uint32]),
+    # pai_llama.h
+    "pai_rmsnorm_f32_async": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_uint64, C.c_float, _vp]),
+    "pai_rope_kv_append_async": (C.c_int32, [_vp] * 8 + [C.c_uint32] * 6 + [_vp]),
+    "pai_attention_workspace_bytes": (C.c_uint64, [C.c_uint32] * 3),
+    "pai_attention_decode_async": (C.c_int32, [_vp] * 5 + [C.c_uint32] * 5 + [_vp]),
+    "pai_argmax_workspace_bytes": (C.c_uint64, []),
+    "pai_argmax_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp]),
+    "pai_llama_create": (C.c_int32, [C.POINTER(C.c_void_p), _vp]),
+    "pai_llama_free": (None, [_vp]),
+    "pai_llama_set_layer": (C.c_int32, [_vp, C.c_uint32] + [_vp] * 9),
+    "pai_llama_set_output": (C.c_int32, [_vp] * 4),
+    "pai_llama_kv_write": (C.c_int32, [_vp, C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp]),
+    "pai_llama_decode": (C.c_int32, [_vp, C.c_uint32, C.c_uint32, _vp, _vp]),
+    "pai_llama_decode_async": (C.c_int32, [_vp, _vp, C.c_uint32, _vp, _vp]),
+    "pai_llama_logits": (C.c_void_p, [_vp]),
+    "pai_llama_kv_cache": (C.c_int32, [_vp, C.c_uint32, C.POINTER(C.c_void_p),
+                                       C.POINTER(C.c_void_p)]),
     # paiq.h
     "paiq_quantize": (C.c_int32, [C.c_uint32, _vp, C.c_uint64, C.c_uint64, _vp, C.c_uint64,
                                   C.c_int]),

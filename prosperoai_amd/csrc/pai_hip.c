@@ -304,6 +304,15 @@ pai_status_t pai_qmat_upload_device(pai_qmat_t **out, uint32_t type, uint64_t n,
   return make_qmat(out, type, n, k, dev_blocks, stream);
 }
 
+/* Shared with pai_llama.c; not exported from the library. */
+__attribute__((visibility("hidden"))) const paik_qview_t *pai__qmat_view(const pai_qmat_t *w) {
+  return &w->view;
+}
+__attribute__((visibility("hidden"))) pai_status_t pai__map_hip(int e, const char *what) {
+  return map_hip((hipError_t)e, what);
+}
+__attribute__((visibility("hidden"))) pai_status_t pai__ready(void) { return ensure_ready(); }
+
 pai_status_t pai_qmat_free(pai_qmat_t *w) {
   if (w == NULL) return PAI_OK;
   if (w->x16 != NULL) (void)hipFree(w->x16);

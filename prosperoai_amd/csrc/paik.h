@@ -78,6 +78,27 @@ int paik_gemv_mx(const paik_qview_t *const *vs, float *const *ys,
                  uint32_t count, uint32_t m, const float *x, void *stream);
 int paik_gemv_mx_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
                           uint32_t m, const float *x, float *h, void *stream);
+
+/* Decode-step kernels (qdecode.hip). kc/vc are fp16 caches [hk][ctx][hd]. */
+uint32_t paik_norm_max(void);
+int paik_add_rmsnorm(float *x, const float *delta, const float *gamma, float *xn,
+                     uint32_t n, float eps, void *stream);
+int paik_rope_append(const float *q, const float *k, const float *v, float *qo,
+                     void *kc, void *vc, const float *cos_t, const float *sin_t,
+                     uint32_t hq, uint32_t hk, uint32_t hd, uint32_t r2,
+                     uint32_t ctx, uint32_t pos, void *stream);
+/* part holds hq * paik_attn_chunks(len) * (hd + 2) floats */
+uint32_t paik_attn_chunks(uint32_t len);
+int paik_attn_decode(const float *q, const void *kc, const void *vc, float *part,
+                     float *o, uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
+                     uint32_t len, void *stream);
+/* pv, pi hold paik_argmax_parts() entries */
+uint32_t paik_argmax_parts(void);
+int paik_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *out,
+                void *stream);
+/* out[0..k) = row *row of the matrix (device index, clamped to n - 1) */
+int paik_dequant_row(const paik_qview_t *v, const uint32_t *row, float *out,
+                     void *stream);
 /* x16 (may be NULL): device workspace of x16_bytes for a 16-bit copy of
  * the activations; with it the activations move into LDS by DMA.
  * gate (may be NULL, may equal y): y = silu(gate) * (x W^T) elementwise,

@@ -1,0 +1,411 @@
+/*
+ * The non-matmul kernels of one LLaMA decode step: the residual add fused
+ * with RMSNorm, RoPE of q and k fused with the fp16 KV-cache append,
+ * grouped-query attention of the new token over the cache (split over the
+ * context, then combined), the token-embedding row and the greedy argmax.
+ * The projections are the packed GEMV kernels (qgemv.hip, qgemv_mx.hip).
+ *
+ * Each kernel follows one of the reference's operators
+ * (cpu/reference/ref_ops.c, models/sampler.c); the KV cache holds fp16
+ * keys and values, so attention reads the cached values widened back to
+ * f32. No FMA contraction in this unit: RMSNorm's two products, RoPE's
+ * products and differences and the row dequantization round like the
+ * reference's C (explicit fmaf only where the order is the build's own).
+ */
+#pragma clang fp contract(off)
+
+#include "qdev.h"
+
+namespace paik {
+namespace dec {
+
+constexpr int kNormThreads = 1024;
+constexpr int kNormPer = 16; /* elements per thread: n <= 16384 */
+
+/* Block-wide sum of a double in a fixed order; every thread gets it. */
+__device__ double block_sum(double v, double *sh) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) sh[wave] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < nw; ++w) t += sh[w];
+  return t;
+}
+
+/* x += delta (when delta is set), then xn = x * gamma * rms with
+ * rms = 1 / sqrtf((float)(sum x^2 / n) + eps), the sum taken in double:
+ * pai_ref_rmsnorm_gamma_f32 (cpu/reference/ref_ops.c:196-218) after the
+ * residual ADD (adapters/llama/llama.c:746-751, :786-791). One workgroup;
+ * each thread keeps its elements in registers between the two passes. */
+__global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm(float *__restrict__ x,
+                                                              const float *__restrict__ delta,
+                                                              const float *__restrict__ gamma,
+                                                              float *__restrict__ xn, uint32_t n,
+                                                              float eps) {
+  __shared__ double sh[kNormThreads / 64];
+  float v[kNormPer];
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < kNormPer; ++j) {
+    const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
+    v[j] = 0.0f;
+    if (i < n) {
+      float t = x[i];
+      if (delta != nullptr) {
+        t = t + delta[i];
+        x[i] = t;
+      }
+      v[j] = t;
+      acc += (double)t * (double)t;
+    }
+  }
+  const double tot = block_sum(acc, sh);
+  const float rms = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+#pragma unroll
+  for (int j = 0; j < kNormPer; ++j) {
+    const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
+    if (i < n) xn[i] = v[j] * gamma[i] * rms;
+  }
+}
+
+/* RoPE at position pos on the heads of q (hq heads) and k (hk heads) of
+ * dimension hd, rotating the pairs (i, i + r2), i < r2, with the f32
+ * tables cos_t/sin_t of that position (pai_ref_rope_f32,
+ * cpu/reference/ref_ops.c:231-256). The rotated q goes to qo; the rotated
+ * k and the v row are rounded to fp16 and stored at position pos of the
+ * caches kc/vc ([hk][ctx][hd]). Workgroup h < hq: q head h; otherwise KV
+ * head h - hq. One thread per element (hd <= 256). */
+__global__ void __launch_bounds__(256) k_rope_append(const float *__restrict__ q,
+                                                     const float *__restrict__ k,
+                                                     const float *__restrict__ v,
+                                                     float *__restrict__ qo,
+                                                     _Float16 *__restrict__ kc,
+                                                     _Float16 *__restrict__ vc,
+                                                     const float *__restrict__ cos_t,
+                                                     const float *__restrict__ sin_t,
+                                                     uint32_t hq, uint32_t hd, uint32_t r2,
+                                                     uint32_t ctx, uint32_t pos) {
+  const uint32_t h = blockIdx.x, i = threadIdx.x;
+  if (i >= hd) return;
+  const bool isq = h < hq;
+  const uint32_t kh = isq ? 0u : h - hq;
+  const float *src = isq ? q + (size_t)h * hd : k + (size_t)kh * hd;
+  float o;
+  if (i < r2) {
+    o = src[i] * cos_t[i] - src[i + r2] * sin_t[i];
+  } else if (i < 2u * r2) {
+    o = src[i - r2] * sin_t[i - r2] + src[i] * cos_t[i - r2];
+  } else {
+    o = src[i];
+  }
+  if (isq) {
+    qo[(size_t)h * hd + i] = o;
+  } else {
+    const size_t at = ((size_t)kh * ctx + pos) * hd + i;
+    kc[at] = (_Float16)o;
+    vc[at] = (_Float16)v[(size_t)kh * hd + i];
+  }
+}
+
+/* Attention of one token over cache positions [0, len):
+ * pai_ref_attention_f32 (cpu/reference/ref_ops.c:287-340) for the last
+ * position. Head h reads KV head h / G with G = hq / hk (the reference's
+ * (h * hk) / hq), scores are (q . k) / sqrtf(hd), softmax subtracts the
+ * maximum, and the output is the probability-weighted sum of v.
+ *
+ * Split over the context: workgroup (kvh, c) covers positions
+ * [64c, 64c + 64) for the G heads of KV head kvh, so each K and V row is
+ * read once for all G heads. A wave takes 16 positions; HD/8 lanes share a
+ * row (16 bytes of fp16 each: one coalesced 256-byte row read for HD=128).
+ * Each wave keeps (max, sum of e^(s-max), sum of e^(s-max) v) per head;
+ * the four waves are merged in LDS and the chunk's triple is written to
+ * part[(kvh*nch + c)*G + g] = {m, l, o[HD]}. */
+constexpr uint32_t kChunk = 64;
+constexpr uint32_t kMaxG = 8;
+
+__device__ __forceinline__ float f16lo(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float f16hi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
+                                                   const _Float16 *__restrict__ kc,
+                                                   const _Float16 *__restrict__ vc,
+                                                   float *__restrict__ part, uint32_t G,
+                                                   uint32_t ctx, uint32_t len, uint32_t nch) {
+  constexpr int LP = HD / 8;   /* lanes per row */
+  constexpr int PPI = 64 / LP; /* rows per wave instruction */
+  constexpr int IT = 16 / PPI; /* iterations over a wave's 16 rows */
+  __shared__ float sm[4][kMaxG], sl[4][kMaxG];
+  __shared__ float so[4][kMaxG][HD];
+  const uint32_t kvh = blockIdx.x / nch, c = blockIdx.x % nch;
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t slot = lane / LP, t = lane % LP;
+  const float scale = 1.0f / sqrtf((float)HD);
+  const _Float16 *kb = kc + (size_t)kvh * ctx * HD;
+  const _Float16 *vb = vc + (size_t)kvh * ctx * HD;
+  const uint32_t base = c * kChunk + wave * 16u;
+
+  /* this lane's rows: 8 K and 8 V values each (fp16 -> f32) */
+  float kr[IT][8], vr[IT][8];
+  bool ok[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const uint32_t p = base + (uint32_t)(it * PPI) + slot;
+    ok[it] = p < len;
+    const uint32_t pc = ok[it] ? p : 0u; /* an in-bounds row for idle lanes */
+    const uint4 kw = *reinterpret_cast<const uint4 *>(kb + (size_t)pc * HD + 8u * t);
+    const uint4 vw = *reinterpret_cast<const uint4 *>(vb + (size_t)pc * HD + 8u * t);
+    const uint32_t ka[4] = {kw.x, kw.y, kw.z, kw.w}, va[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      kr[it][2 * e] = f16lo(ka[e]);
+      kr[it][2 * e + 1] = f16hi(ka[e]);
+      vr[it][2 * e] = f16lo(va[e]);
+      vr[it][2 * e + 1] = f16hi(va[e]);
+    }
+  }
+
+  for (uint32_t g = 0; g < G; ++g) {
+    const float *qh = q + (size_t)(kvh * G + g) * HD + 8u * t;
+    float qv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = qh[e];
+    float s[IT];
+    float m = -INFINITY;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kr[it][e], d);
+#pragma unroll
+      for (int o = LP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+      s[it] = ok[it] ? d * scale : -INFINITY;
+      m = fmaxf(m, s[it]);
+    }
+#pragma unroll
+    for (int o = 32; o >= LP; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float l = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const float e = ok[it] ? expf(s[it] - m) : 0.0f;
+      l += e;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, vr[it][j], acc[j]);
+    }
+#pragma unroll
+    for (int o = 32; o >= LP; o >>= 1) {
+      l += __shfl_xor(l, o, 64);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += __shfl_xor(acc[j], o, 64);
+    }
+    if (slot == 0u) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) so[wave][g][8u * t + j] = acc[j];
+      if (t == 0u) {
+        sm[wave][g] = m;
+        sl[wave][g] = l;
+      }
+    }
+  }
+  __syncthreads();
+  /* merge the four waves (a wave with no valid row has m = -inf, l = 0) */
+  float *out = part + (size_t)blockIdx.x * G * (HD + 2u);
+  for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
+    const uint32_t g = e / HD, d = e % HD;
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][g]);
+    float L = 0.0f, O = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+      const float f = sm[w][g] == -INFINITY ? 0.0f : expf(sm[w][g] - M);
+      L = fmaf(sl[w][g], f, L);
+      O = fmaf(so[w][g][d], f, O);
+    }
+    out[g * (HD + 2u) + 2u + d] = O;
+    if (d == 0u) {
+      out[g * (HD + 2u)] = M;
+      out[g * (HD + 2u) + 1u] = L;
+    }
+  }
+}
+
+/* Merge the chunks of each head: M = max m_c, L = sum l_c e^(m_c - M),
+ * o = (sum o_c e^(m_c - M)) / L, chunks in order. One workgroup per q head;
+ * every chunk holds at least one position, so each m_c is finite. */
+__global__ void __launch_bounds__(256) k_attn_combine(const float *__restrict__ part,
+                                                      float *__restrict__ o, uint32_t G,
+                                                      uint32_t hd, uint32_t nch) {
+  const uint32_t h = blockIdx.x, kvh = h / G, g = h % G;
+  const size_t stride = (size_t)G * (hd + 2u);
+  const float *p0 = part + (size_t)kvh * nch * stride + (size_t)g * (hd + 2u);
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, p0[c * stride]);
+  float L = 0.0f;
+  for (uint32_t c = 0; c < nch; ++c) L = fmaf(p0[c * stride + 1u], expf(p0[c * stride] - M), L);
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < nch; ++c)
+      acc = fmaf(p0[c * stride + 2u + d], expf(p0[c * stride] - M), acc);
+    o[(size_t)h * hd + d] = acc / L;
+  }
+}
+
+/* Greedy token: the first index of the largest logit, as the reference's
+ * scan `if (p[i] > best)` from best = p[0] (models/sampler.c:146-155):
+ * NaNs after index 0 never win, and a NaN at index 0 wins outright. Two
+ * passes: per-workgroup (value, index) pairs, then one workgroup over
+ * them. */
+constexpr uint32_t kArgParts = 256;
+
+__device__ void better(float &v, uint32_t &i, float v2, uint32_t i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__device__ void block_best(float &v, uint32_t &i, float *shv, uint32_t *shi) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(v, o, 64);
+    const uint32_t i2 = (uint32_t)__shfl_xor((int)i, o, 64);
+    better(v, i, v2, i2);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    shv[wave] = v;
+    shi[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(v, i, shv[w], shi[w]);
+}
+
+__global__ void __launch_bounds__(256) k_argmax_part(const float *__restrict__ x, uint32_t n,
+                                                     float *__restrict__ pv,
+                                                     uint32_t *__restrict__ pi) {
+  __shared__ float shv[4];
+  __shared__ uint32_t shi[4];
+  float v = -INFINITY;
+  uint32_t i = 0xFFFFFFFFu;
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x)
+    better(v, i, x[j], j);
+  block_best(v, i, shv, shi);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = v;
+    pi[blockIdx.x] = i;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_argmax_final(const float *__restrict__ x,
+                                                      const float *__restrict__ pv,
+                                                      const uint32_t *__restrict__ pi,
+                                                      uint32_t *__restrict__ out) {
+  __shared__ float shv[4];
+  __shared__ uint32_t shi[4];
+  float v = -INFINITY;
+  uint32_t i = 0xFFFFFFFFu;
+  for (uint32_t j = threadIdx.x; j < kArgParts; j += blockDim.x) better(v, i, pv[j], pi[j]);
+  block_best(v, i, shv, shi);
+  if (threadIdx.x == 0) {
+    const float x0 = x[0];
+    /* x0 is NaN, or every logit is NaN: the reference keeps index 0 */
+    out[0] = (x0 != x0 || i == 0xFFFFFFFFu) ? 0u : i;
+  }
+}
+
+/* Row `*row` of a packed matrix, dequantized exactly: the token-embedding
+ * lookup (the reference multiplies a one-hot row by the dequantized
+ * token_embd, adapters/llama/llama.c:511-520, which selects that row
+ * exactly). One thread per chunk; a row index past the end reads the last
+ * row. */
+template <class F>
+__global__ void __launch_bounds__(256) k_dequant_row(paik_qview_t v,
+                                                     const uint32_t *__restrict__ row_p,
+                                                     float *__restrict__ out) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= (v.k >> 5)) return;
+  const uint32_t row = min(row_p[0], v.n - 1u);
+  float o[32];
+  F::dequant(F::load(v, row, c), c, o);
+  float4 *dst = reinterpret_cast<float4 *>(out + 32u * c);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dst[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+} // namespace dec
+} // namespace paik
+
+using namespace paik;
+using namespace paik::dec;
+
+extern "C" uint32_t paik_norm_max(void) { return (uint32_t)(kNormPer * kNormThreads); }
+
+extern "C" int paik_add_rmsnorm(float *x, const float *delta, const float *gamma, float *xn,
+                                uint32_t n, float eps, void *stream) {
+  if (n == 0u || n > paik_norm_max()) return (int)hipErrorInvalidValue;
+  k_add_rmsnorm<<<1, kNormThreads, 0, (hipStream_t)stream>>>(x, delta, gamma, xn, n, eps);
+  return (int)hipGetLastError();
+}
+
+extern "C" int paik_rope_append(const float *q, const float *k, const float *v, float *qo,
+                                void *kc, void *vc, const float *cos_t, const float *sin_t,
+                                uint32_t hq, uint32_t hk, uint32_t hd, uint32_t r2, uint32_t ctx,
+                                uint32_t pos, void *stream) {
+  if (hd == 0u || hd > 256u || r2 == 0u || 2u * r2 > hd || pos >= ctx)
+    return (int)hipErrorInvalidValue;
+  k_rope_append<<<hq + hk, 256, 0, (hipStream_t)stream>>>(
+      q, k, v, qo, static_cast<_Float16 *>(kc), static_cast<_Float16 *>(vc), cos_t, sin_t, hq, hd,
+      r2, ctx, pos);
+  return (int)hipGetLastError();
+}
+
+extern "C" uint32_t paik_attn_chunks(uint32_t len) { return (len + kChunk - 1u) / kChunk; }
+
+extern "C" int paik_attn_decode(const float *q, const void *kc, const void *vc, float *part,
+                                float *o, uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
+                                uint32_t len, void *stream) {
+  if (hk == 0u || hq % hk != 0u || hq / hk > kMaxG || len == 0u || len > ctx)
+    return (int)hipErrorInvalidValue;
+  const uint32_t G = hq / hk, nch = paik_attn_chunks(len);
+  hipStream_t s = (hipStream_t)stream;
+  const _Float16 *k16 = static_cast<const _Float16 *>(kc);
+  const _Float16 *v16 = static_cast<const _Float16 *>(vc);
+  switch (hd) {
+  case 64: k_attn_part<64><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
+  case 128: k_attn_part<128><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
+  case 256: k_attn_part<256><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
+  default: return (int)hipErrorInvalidValue;
+  }
+  k_attn_combine<<<hq, 256, 0, s>>>(part, o, G, hd, nch);
+  return (int)hipGetLastError();
+}
+
+extern "C" uint32_t paik_argmax_parts(void) { return kArgParts; }
+
+extern "C" int paik_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *out,
+                           void *stream) {
+  if (n == 0u) return (int)hipErrorInvalidValue;
+  hipStream_t s = (hipStream_t)stream;
+  k_argmax_part<<<kArgParts, 256, 0, s>>>(x, n, pv, pi);
+  k_argmax_final<<<1, 256, 0, s>>>(x, pv, pi, out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int paik_dequant_row(const paik_qview_t *v, const uint32_t *row, float *out,
+                                void *stream) {
+  const uint32_t nc = v->k >> 5;
+  const dim3 grid((nc + 255u) / 256u), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (v->type) {
+  case 8u: k_dequant_row<Q8_0><<<grid, block, 0, s>>>(*v, row, out); break;
+  case 2u: k_dequant_row<Q4_0><<<grid, block, 0, s>>>(*v, row, out); break;
+  case 12u: k_dequant_row<Q4_K><<<grid, block, 0, s>>>(*v, row, out); break;
+  case 14u: k_dequant_row<Q6_K><<<grid, block, 0, s>>>(*v, row, out); break;
+  default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}

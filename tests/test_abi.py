@@ -123,3 +123,36 @@ def test_init_without_gpu_reports_init_error():
     h = C.c_void_p()
     blocks = np.zeros(18, np.uint8)
     assert pa.lib().pai_qmat_upload(C.byref(h), 2, 1, 32, blocks.ctypes.data, 18) == -8
+
+
+def test_decode_entry_points_reject_bad_arguments_before_device():
+    """pai_llama.h: shape and argument errors come back before any device
+    work (these run without a GPU)."""
+    from prosperoai_amd.llama import LlamaConfig
+    lib = pa.lib()
+    fake = C.c_void_p(0x1000)  # never dereferenced: validation fails first
+    h = C.c_void_p()
+    base = dict(n_layer=1, n_embd=256, n_head=4, n_head_kv=2, n_ff=512, vocab=100, ctx=8, n_rot=0,
+                rope_theta=0.0, norm_eps=0.0)
+    for change, want in (({"n_head_kv": 3}, -1), ({"n_embd": 384, "n_head": 4}, -3),
+                         ({"n_head": 16, "n_head_kv": 1, "n_embd": 1024}, -3), ({"ctx": 0}, -1),
+                         ({"n_embd": 20480, "n_head": 160, "n_head_kv": 20}, -3)):
+        cfg = LlamaConfig(**{**base, **change})
+        assert lib.pai_llama_create(C.byref(h), C.byref(cfg)) == want, change
+    assert lib.pai_llama_create(None, None) == -1
+    # attention: head size, GQA ratio, length
+    assert lib.pai_attention_decode_async(fake, fake, fake, fake, fake, 8, 2, 100, 64, 8, None) == -3
+    assert lib.pai_attention_decode_async(fake, fake, fake, fake, fake, 8, 3, 64, 64, 8, None) == -1
+    assert lib.pai_attention_decode_async(fake, fake, fake, fake, fake, 32, 2, 64, 64, 8, None) == -3
+    assert lib.pai_attention_decode_async(fake, fake, fake, fake, fake, 8, 2, 64, 64, 65, None) == -1
+    assert lib.pai_attention_decode_async(fake, fake, fake, fake, fake, 8, 2, 64, 64, 0, None) == -1
+    # rope: position outside the cache, rotation wider than the head
+    args = [fake] * 8
+    assert lib.pai_rope_kv_append_async(*args, 4, 2, 64, 32, 16, 16, None) == -1
+    assert lib.pai_rope_kv_append_async(*args, 4, 2, 64, 40, 16, 0, None) == -3
+    assert lib.pai_rope_kv_append_async(*args, 4, 2, 512, 32, 16, 0, None) == -3
+    # norm and argmax sizes
+    assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 0, 0.0, None) == -1
+    assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 16385, 0.0, None) == -3
+    assert lib.pai_argmax_f32_async(fake, 0, fake, fake, None) == -1
+    assert lib.pai_attention_workspace_bytes(32, 128, 2048) == 32 * 32 * 130 * 4
