@@ -24,7 +24,10 @@ extra    = the seven projections as separate launches; the step with
            silu(gate)*up fused into the gate/up launch; Q4_K at M in
            {1, 8, 32}; Q8_0 4096x4096 GEMV; and the M=512 prefill GEMMs
            (gate Q4_K, down Q6_K, and gate+up with the fused silu*mul) in
-           TFLOP/s against 2.5 PFLOP/s dense fp16.
+           TFLOP/s against 2.5 PFLOP/s dense fp16; and the full decode step
+           of a Llama-3-8B-shape model with an fp16 KV cache at context
+           2048 (ms/token, and GB/s over its weight, cache and embedding
+           bytes).
 """
 from __future__ import annotations
 
@@ -297,6 +300,117 @@ def prefill(pa, hm, reps: int) -> dict:
     return out
 
 
+DECODE_SHAPES = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+                 "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+
+
+def decode_8b(pa, hm, steps: int, warmup: int, fill: int = 2048, threads: int = 8) -> dict:
+    """One greedy decode step of a random-init Llama-3-8B-shape model
+    (32 layers, hidden 4096, 32/8 heads, FFN 14336, vocab 128256, RoPE
+    theta 500000) with the fp16 KV cache prefilled to `fill` positions.
+    Q4_K weights, Q6_K ffn_down and output head, N(0, 0.02^2) per matrix
+    from its own seed; norms 1; cache N(0, 1). Steps run on one stream,
+    the token passed on the device from step to step (eager launches), and
+    again as one captured step replayed (HIP graph)."""
+    import concurrent.futures as cf
+    from prosperoai_amd.llama import Llama, LlamaConfig
+    cfg = LlamaConfig(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, n_ff=14336,
+                      vocab=128256, ctx=fill + warmup + steps + 2, n_rot=0,
+                      rope_theta=500000.0, norm_eps=0.0)
+    t0 = time.time()
+    qt = {n: (pa.Q6_K if n == "down" else pa.Q4_K) for n in DECODE_SHAPES}
+
+    def make(job):
+        name, n, k, seed, qtype = job
+        w = pa.normal_f32(seed, n * k, 0.0, 0.02).reshape(n, k)
+        return job, pa.quantize(qtype, w, 1)
+
+    jobs = [(nm, n, k, seed_w(5, 0) + 64 * L + i, qt[nm])
+            for L in range(cfg.n_layer) for i, (nm, (n, k)) in enumerate(DECODE_SHAPES.items())]
+    rows = 128256 // 8  # the two vocab matrices in 8 row bands each
+    for name, qtype, base in (("token_embd", pa.Q4_K, 1 << 20), ("output", pa.Q6_K, 1 << 21)):
+        jobs += [(f"{name}:{b}", rows, 4096, seed_w(5, 0) + base + b, qtype) for b in range(8)]
+    m = Llama(cfg)
+    mats, bands = {}, {}
+    weight_bytes = 0
+    with cf.ThreadPoolExecutor(threads) as ex:
+        for (name, n, k, seed, qtype), blocks in ex.map(make, jobs):
+            if ":" in name:
+                bands[name] = (qtype, blocks)
+                continue
+            L = (seed - seed_w(5, 0)) // 64
+            mats[(L, name)] = pa.QMat(qtype, n, k, blocks)
+            weight_bytes += blocks.nbytes
+            if all((L, nm) in mats for nm in DECODE_SHAPES):
+                m.set_layer(L, {nm: mats[(L, nm)] for nm in DECODE_SHAPES},
+                            np.ones(4096, np.float32), np.ones(4096, np.float32))
+    head = {}
+    for name in ("token_embd", "output"):
+        qtype = bands[f"{name}:0"][0]
+        blocks = np.concatenate([bands[f"{name}:{b}"][1] for b in range(8)])
+        head[name] = pa.QMat(qtype, 128256, 4096, blocks)
+        if name == "output":
+            weight_bytes += blocks.nbytes
+    bands.clear()
+    m.set_output(head["token_embd"], head["output"], np.ones(4096, np.float32))
+    rng = np.random.default_rng(seed_w(5, 15))
+    for L in range(cfg.n_layer):
+        k = rng.standard_normal((fill, 8, 128), dtype=np.float32).astype(np.float16)
+        v = rng.standard_normal((fill, 8, 128), dtype=np.float32).astype(np.float16)
+        m.kv_write(L, 0, k, v)
+    setup_s = time.time() - t0
+    log(f"decode 8B: model built in {setup_s:.1f} s")
+
+    tok = hm.DeviceBuffer.from_array(np.array([1, 0], np.uint32))
+    st = hm.Stream()
+
+    def step(pos, sh):  # step pos reads slot pos % 2, writes the other
+        m.decode_async(tok.ptr + 4 * (pos % 2), pos, tok.ptr + 4 * ((pos + 1) % 2), sh)
+
+    for i in range(warmup):
+        step(fill + i, st.handle)
+    st.synchronize()
+    a, b = hm.Event(), hm.Event()
+    a.record(st)
+    for i in range(steps):
+        step(fill + warmup + i, st.handle)
+    b.record(st)
+    b.synchronize()
+    eager_ms = a.elapsed_ms(b) / steps
+    # one captured step at a fixed position, replayed
+    pos_g = fill + warmup + steps
+    g = hm.Graph(st, lambda sh: step(pos_g, sh))
+    g.launch(st)
+    st.synchronize()
+    a.record(st)
+    for _ in range(steps):
+        g.launch(st)
+    b.record(st)
+    b.synchronize()
+    graph_ms = a.elapsed_ms(b) / steps
+    # the last step's token is the argmax of its logits, and they are finite
+    logits = np.empty(cfg.vocab, np.float32)
+    hm.hip_check(hm.hip().hipMemcpy(logits.ctypes.data, m.logits_ptr(), logits.nbytes, hm.D2H),
+                 "logits")
+    nxt = int(tok.download(2, np.uint32)[(pos_g + 1) % 2])
+    ok = bool(np.isfinite(logits).all() and nxt == int(np.argmax(logits)))
+    kv_bytes = 32 * 2 * 8 * 128 * 2 * (fill + warmup + steps // 2 + 1)  # mean cache read
+    emb_row = pa.qtype_bytes(pa.Q4_K, 4096)
+    step_bytes = weight_bytes + kv_bytes + emb_row
+    out = {"ms_per_token": round(eager_ms, 4), "tokens_per_s": round(1e3 / eager_ms, 1),
+           "GBps": round(step_bytes / (eager_ms * 1e-3) / 1e9, 1),
+           "frac_hbm": round(step_bytes / (eager_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "graph_ms_per_token": round(graph_ms, 4),
+           "graph_GBps": round(step_bytes / (graph_ms * 1e-3) / 1e9, 1),
+           "bytes_per_token": step_bytes, "weight_bytes": weight_bytes, "kv_bytes": kv_bytes,
+           "context": fill, "steps": steps, "argmax_ok": ok, "setup_s": round(setup_s, 1)}
+    g.destroy(); a.destroy(); b.destroy(); st.destroy(); tok.free()
+    m.free()
+    for w in list(mats.values()) + list(head.values()):
+        w.free()
+    return out
+
+
 def cpu_baseline(pa, budget_s: float) -> dict:
     """The reference's single-thread AVX2 GEMV on dequantized f32 weights of
     the seven Q4_0 projections (bounded number of passes)."""
@@ -437,6 +551,9 @@ def main() -> int:
                     help="skip the per-launch timings of the headline step")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with device copies of this size (counter calibration)")
+    ap.add_argument("--decode-only", type=int, metavar="STEPS", default=0,
+                    help="run only the full-model decode step (Llama-3-8B shape, fp16 KV "
+                         "cache at context 2048) for STEPS timed steps and print its JSON")
     ap.add_argument("--trace-summary", metavar="TRACE_CSV",
                     help="summarise the headline's timed-region GEMV dispatches of a "
                          "rocprofv3 --kernel-trace CSV of a run with the same --steps, "
@@ -461,6 +578,9 @@ def main() -> int:
     import prosperoai_amd as pa
     from prosperoai_amd import hipmem as hm
     pa.init()
+    if args.decode_only:
+        print(json.dumps(decode_8b(pa, hm, args.decode_only, 5)), flush=True)
+        return 0
     log(f"Q4_0 M=1 x {args.layers} layers")
 
     head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup,
@@ -502,6 +622,8 @@ def main() -> int:
             log(f"Q4_0 M=1 host pointers: {extra['q4_0_m1_host_pointers']}")
             extra["prefill_m512"] = prefill(pa, hm, 20)
             log(f"prefill: {extra['prefill_m512']}")
+            extra["decode_8b_ctx2048"] = decode_8b(pa, hm, 20, 5)
+            log(f"decode 8B: {extra['decode_8b_ctx2048']}")
         except Exception as e:  # extras never hide the headline
             extra["error"] = repr(e)
     if args.calib_copy_mib:

@@ -54,8 +54,11 @@ pai_status_t pai_rope_kv_append_async(const float *q, const float *k, const floa
                                       uint32_t hk, uint32_t hd, uint32_t r2, uint32_t ctx,
                                       uint32_t pos, void *stream);
 
-/* Bytes of the workspace pai_attention_decode_async needs for hq heads of
- * dimension hd over len positions. */
+/* Bytes of the workspace the attention calls need for hq heads of
+ * dimension hd over len positions. The workspace (256-byte aligned) must be
+ * zero-filled before its first use; every call leaves it fit for the next
+ * (its per-KV-head counters return to zero). Calls sharing a workspace
+ * must not overlap. */
 uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len);
 
 /* Attention of one query position over cache positions 0..len-1:
@@ -63,12 +66,31 @@ uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len);
  * head h reading KV head h / (hq / hk). The last row of
  * pai_ref_attention_f32 (cpu/reference/ref_ops.c:287-340) with keys and
  * values taken from the fp16 caches ([hk][ctx][hd]). hd in {64, 128, 256},
- * hq / hk <= 8, 1 <= len <= ctx. The dot products and sums run in another
- * order (and with FMA): rel-L2 <= 1e-5 against the reference's formula. */
+ * hq / hk <= 8, hk <= 256, 1 <= len <= min(ctx, 32768). One launch: the
+ * context is split in chunks of 64 positions, and the last chunk of each
+ * KV head to finish merges that head group's chunks. The dot products and
+ * sums run in another order (and with FMA) than the reference's: rel-L2
+ * <= 1e-5 against its formula where scores are O(1); for large scores,
+ * where the reference's own f32 evaluation errs by as much, within twice
+ * its error against a float64 evaluation. */
 pai_status_t pai_attention_decode_async(const float *q, const void *k_cache,
                                         const void *v_cache, float *out, void *workspace,
                                         uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
                                         uint32_t len, void *stream);
+
+/* The decode step's attention block in one launch: RoPE of q and k at
+ * position pos (as pai_rope_kv_append_async, bit for bit), the append of
+ * the rotated k and of v at pos (fp16), and pai_attention_decode_async over
+ * positions 0..pos. q: [hq][hd] and k, v: [hk][hd] as the projections
+ * produce them (not rotated); cos_t, sin_t: the r2 table entries of
+ * position pos. Replaces the reference's ROPE(q), ROPE(k), ATTENTION ops
+ * of one layer (adapters/llama/llama.c:713-733) for the last position. */
+pai_status_t pai_attention_decode_rope_async(const float *q, const float *k, const float *v,
+                                             const float *cos_t, const float *sin_t, uint32_t r2,
+                                             void *k_cache, void *v_cache, float *out,
+                                             void *workspace, uint32_t hq, uint32_t hk,
+                                             uint32_t hd, uint32_t ctx, uint32_t pos,
+                                             void *stream);
 
 /* Bytes of the workspace pai_argmax_f32_async needs. */
 uint64_t pai_argmax_workspace_bytes(void);
@@ -91,7 +113,7 @@ typedef struct pai_llama_config {
   uint32_t n_head_kv; /* key/value heads: divides n_head, n_head / n_head_kv <= 8 */
   uint32_t n_ff;      /* feed-forward size */
   uint32_t vocab;     /* logits */
-  uint32_t ctx;       /* cache positions */
+  uint32_t ctx;       /* cache positions (<= 32768) */
   uint32_t n_rot;     /* rotated dimensions per head; 0, odd or above the head
                          size means the head size (adapters/llama/llama.c:372-375) */
   float rope_theta;   /* RoPE base; 0 = 10000 (llama.c:349-352) */

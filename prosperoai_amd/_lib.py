@@ -58,6 +58,8 @@ SIGNATURES = {
     "pai_rope_kv_append_async": (C.c_int32, [_vp] * 8 + [C.c_uint32] * 6 + [_vp]),
     "pai_attention_workspace_bytes": (C.c_uint64, [C.c_uint32] * 3),
     "pai_attention_decode_async": (C.c_int32, [_vp] * 5 + [C.c_uint32] * 5 + [_vp]),
+    "pai_attention_decode_rope_async": (C.c_int32, [_vp] * 5 + [C.c_uint32] + [_vp] * 4
+                                        + [C.c_uint32] * 5 + [_vp]),
     "pai_argmax_workspace_bytes": (C.c_uint64, []),
     "pai_argmax_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp]),
     "pai_llama_create": (C.c_int32, [C.POINTER(C.c_void_p), _vp]),

@@ -72,28 +72,63 @@ pai_status_t pai_rope_kv_append_async(const float *q, const float *k, const floa
   return PAI_OK;
 }
 
+#define ATTN_COUNTER_BYTES 1024u /* one uint32 per KV head, up to 256 */
+
 uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len) {
-  return (uint64_t)hq * paik_attn_chunks(len) * ((uint64_t)hd + 2u) * sizeof(float);
+  return ATTN_COUNTER_BYTES +
+         (uint64_t)hq * paik_attn_chunks(len) * ((uint64_t)hd + 2u) * sizeof(float);
 }
 
-pai_status_t pai_attention_decode_async(const float *q, const void *k_cache, const void *v_cache,
-                                        float *out, void *workspace, uint32_t hq, uint32_t hk,
-                                        uint32_t hd, uint32_t ctx, uint32_t len, void *stream) {
+static pai_status_t check_attention(const float *q, const void *k_cache, const void *v_cache,
+                                    const float *out, const void *workspace, uint32_t hq,
+                                    uint32_t hk, uint32_t hd, uint32_t ctx, uint32_t len) {
   if (q == NULL || k_cache == NULL || v_cache == NULL || out == NULL || workspace == NULL)
     return fail(PAI_ERR_INVALID_ARG, "NULL argument");
   if (hq == 0u || hk == 0u || hd == 0u || ctx == 0u || len == 0u)
     return fail(PAI_ERR_INVALID_ARG, "zero size");
   if (hq % hk != 0u) return fail(PAI_ERR_INVALID_ARG, "hq=%u not a multiple of hk=%u", hq, hk);
   if (hq / hk > 8u) return fail(PAI_ERR_UNSUPPORTED, "hq / hk = %u above 8", hq / hk);
+  if (hk > ATTN_COUNTER_BYTES / 4u) return fail(PAI_ERR_UNSUPPORTED, "hk=%u above 256", hk);
   if (hd != 64u && hd != 128u && hd != 256u)
     return fail(PAI_ERR_UNSUPPORTED, "head size %u (64, 128 or 256)", hd);
   if (len > ctx) return fail(PAI_ERR_INVALID_ARG, "len=%u above ctx=%u", len, ctx);
+  if (len > paik_attn_max_len())
+    return fail(PAI_ERR_UNSUPPORTED, "len=%u above %u", len, paik_attn_max_len());
   if (((uintptr_t)q & 15u) != 0u || ((uintptr_t)k_cache & 15u) != 0u ||
-      ((uintptr_t)v_cache & 15u) != 0u)
-    return fail(PAI_ERR_INVALID_ARG, "q and the caches must be 16-byte aligned");
-  TRY(pai__ready());
-  LAUNCH(paik_attn_decode(q, k_cache, v_cache, (float *)workspace, out, hq, hk, hd, ctx, len,
-                          stream),
+      ((uintptr_t)v_cache & 15u) != 0u || ((uintptr_t)workspace & 255u) != 0u)
+    return fail(PAI_ERR_INVALID_ARG,
+                "q and the caches must be 16-byte aligned, the workspace 256-byte aligned");
+  return pai__ready();
+}
+
+pai_status_t pai_attention_decode_async(const float *q, const void *k_cache, const void *v_cache,
+                                        float *out, void *workspace, uint32_t hq, uint32_t hk,
+                                        uint32_t hd, uint32_t ctx, uint32_t len, void *stream) {
+  TRY(check_attention(q, k_cache, v_cache, out, workspace, hq, hk, hd, ctx, len));
+  char *ws = (char *)workspace;
+  LAUNCH(paik_attn_decode(q, NULL, NULL, NULL, NULL, 0u, (void *)k_cache, (void *)v_cache,
+                          (float *)(ws + ATTN_COUNTER_BYTES), (uint32_t *)ws, out, hq, hk, hd, ctx,
+                          len, stream),
+         "attention launch");
+  return PAI_OK;
+}
+
+pai_status_t pai_attention_decode_rope_async(const float *q, const float *k, const float *v,
+                                             const float *cos_t, const float *sin_t, uint32_t r2,
+                                             void *k_cache, void *v_cache, float *out,
+                                             void *workspace, uint32_t hq, uint32_t hk,
+                                             uint32_t hd, uint32_t ctx, uint32_t pos,
+                                             void *stream) {
+  if (k == NULL || v == NULL || cos_t == NULL || sin_t == NULL)
+    return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  if (pos >= ctx) return fail(PAI_ERR_INVALID_ARG, "pos=%u outside the cache (ctx=%u)", pos, ctx);
+  if (r2 == 0u || 2u * r2 > hd)
+    return fail(PAI_ERR_UNSUPPORTED, "r2=%u: need 1 <= r2 and 2 r2 <= hd=%u", r2, hd);
+  TRY(check_attention(q, k_cache, v_cache, out, workspace, hq, hk, hd, ctx, pos + 1u));
+  char *ws = (char *)workspace;
+  LAUNCH(paik_attn_decode(q, k, v, cos_t, sin_t, r2, k_cache, v_cache,
+                          (float *)(ws + ATTN_COUNTER_BYTES), (uint32_t *)ws, out, hq, hk, hd, ctx,
+                          pos + 1u, stream),
          "attention launch");
   return PAI_OK;
 }
@@ -133,7 +168,7 @@ struct pai_llama {
   void *dev;
   float *norms; /* attn_norm[L], ffn_norm[L], output_norm: (2 L + 1) * n_embd */
   float *cos_t, *sin_t;
-  float *x, *xn, *q, *k, *v, *qr, *a, *o, *h, *d, *logits;
+  float *x, *xn, *q, *k, *v, *a, *o, *h, *d, *logits;
   void *attn_ws, *arg_ws;
   uint32_t *tok; /* [0] token in, [1] next out (synchronous form) */
   void *kv;      /* fp16 [n_layer][2][n_head_kv][ctx][hd] */
@@ -151,6 +186,8 @@ static pai_status_t check_config(const pai_llama_config_t *c, uint32_t *hd) {
   *hd = c->n_embd / c->n_head;
   if (*hd != 64u && *hd != 128u && *hd != 256u)
     return fail(PAI_ERR_UNSUPPORTED, "head size %u (64, 128 or 256)", *hd);
+  if (c->ctx > paik_attn_max_len())
+    return fail(PAI_ERR_UNSUPPORTED, "ctx=%u above %u", c->ctx, paik_attn_max_len());
   if (c->n_embd > paik_norm_max() || c->n_ff > 0x40000000u)
     return fail(PAI_ERR_UNSUPPORTED, "n_embd=%u above %u", c->n_embd, paik_norm_max());
   return PAI_OK;
@@ -198,7 +235,7 @@ pai_status_t pai_llama_create(pai_llama_t **out, const pai_llama_config_t *cfg) 
       (2u * (uint64_t)L + 1u) * E * 4u,                          /* norms */
       (uint64_t)cfg->ctx * m->r2 * 4u,                           /* cos */
       (uint64_t)cfg->ctx * m->r2 * 4u,                           /* sin */
-      E * 4u, E * 4u, QD * 4u, KV * 4u, KV * 4u, QD * 4u,        /* x xn q k v qr */
+      E * 4u, E * 4u, QD * 4u, KV * 4u, KV * 4u,                 /* x xn q k v */
       QD * 4u, E * 4u, (uint64_t)cfg->n_ff * 4u, E * 4u,         /* a o h d */
       (uint64_t)cfg->vocab * 4u,                                 /* logits */
       pai_attention_workspace_bytes(cfg->n_head, hd, cfg->ctx),  /* attention */
@@ -228,15 +265,14 @@ pai_status_t pai_llama_create(pai_llama_t **out, const pai_llama_config_t *cfg) 
   m->q = (float *)p[5];
   m->k = (float *)p[6];
   m->v = (float *)p[7];
-  m->qr = (float *)p[8];
-  m->a = (float *)p[9];
-  m->o = (float *)p[10];
-  m->h = (float *)p[11];
-  m->d = (float *)p[12];
-  m->logits = (float *)p[13];
-  m->attn_ws = p[14];
-  m->arg_ws = p[15];
-  m->tok = (uint32_t *)p[16];
+  m->a = (float *)p[8];
+  m->o = (float *)p[9];
+  m->h = (float *)p[10];
+  m->d = (float *)p[11];
+  m->logits = (float *)p[12];
+  m->attn_ws = p[13];
+  m->arg_ws = p[14];
+  m->tok = (uint32_t *)p[15];
 
   /* KV cache */
   m->kv_layer_bytes = 2u * (uint64_t)cfg->n_head_kv * cfg->ctx * hd * 2u;
@@ -403,11 +439,10 @@ pai_status_t pai_llama_decode_async(pai_llama_t *m, const uint32_t *token_dev, u
       TRY(pai_qgemm_f32_async(w[W_V], 1, m->xn, m->v, f, stream));
     }
     uint16_t *kc = cache_of(m, l, 0), *vc = cache_of(m, l, 1);
-    TRY(pai_rope_kv_append_async(m->q, m->k, m->v, m->qr, kc, vc, m->cos_t + (size_t)pos * m->r2,
-                                 m->sin_t + (size_t)pos * m->r2, hq, hk, hd, m->r2, c->ctx, pos,
-                                 stream));
-    TRY(pai_attention_decode_async(m->qr, kc, vc, m->a, m->attn_ws, hq, hk, hd, c->ctx, pos + 1u,
-                                   stream));
+    /* RoPE, cache append and attention in one launch */
+    TRY(pai_attention_decode_rope_async(m->q, m->k, m->v, m->cos_t + (size_t)pos * m->r2,
+                                        m->sin_t + (size_t)pos * m->r2, m->r2, kc, vc, m->a,
+                                        m->attn_ws, hq, hk, hd, c->ctx, pos, stream));
     TRY(pai_qgemm_f32_async(w[W_O], 1, m->a, m->o, f, stream));
     /* x += o; xn = rmsnorm(x, ffn_norm) */
     TRY(pai_rmsnorm_f32_async(m->x, m->o, m->norms + ((size_t)c->n_layer + l) * E, m->xn, E, eps,

@@ -87,11 +87,17 @@ int paik_rope_append(const float *q, const float *k, const float *v, float *qo,
                      void *kc, void *vc, const float *cos_t, const float *sin_t,
                      uint32_t hq, uint32_t hk, uint32_t hd, uint32_t r2,
                      uint32_t ctx, uint32_t pos, void *stream);
-/* part holds hq * paik_attn_chunks(len) * (hd + 2) floats */
+/* Attention over cache positions [0, len). With knew/vnew set, RoPE of q
+ * and knew (tables of position len - 1) and the append of knew, vnew at
+ * position len - 1 happen in the same launch. part holds
+ * hq * paik_attn_chunks(len) * (hd + 2) floats; counters holds hk zeros
+ * (left zero by every call). len <= paik_attn_max_len(). */
 uint32_t paik_attn_chunks(uint32_t len);
-int paik_attn_decode(const float *q, const void *kc, const void *vc, float *part,
-                     float *o, uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
-                     uint32_t len, void *stream);
+uint32_t paik_attn_max_len(void);
+int paik_attn_decode(const float *q, const float *knew, const float *vnew,
+                     const float *cos_t, const float *sin_t, uint32_t r2, void *kc,
+                     void *vc, float *part, uint32_t *counters, float *o, uint32_t hq,
+                     uint32_t hk, uint32_t hd, uint32_t ctx, uint32_t len, void *stream);
 /* pv, pi hold paik_argmax_parts() entries */
 uint32_t paik_argmax_parts(void);
 int paik_argmax(const float *x, uint32_t n, float *pv, uint32_t *pi, uint32_t *out,

@@ -19,8 +19,8 @@
 namespace paik {
 namespace dec {
 
-constexpr int kNormThreads = 1024;
-constexpr int kNormPer = 16; /* elements per thread: n <= 16384 */
+constexpr int kNormThreads = 256;
+constexpr int kNormVec = 16; /* float4 groups per thread: n <= 16384 */
 
 /* Block-wide sum of a double in a fixed order; every thread gets it. */
 __device__ double block_sum(double v, double *sh) {
@@ -37,36 +37,77 @@ __device__ double block_sum(double v, double *sh) {
  * rms = 1 / sqrtf((float)(sum x^2 / n) + eps), the sum taken in double:
  * pai_ref_rmsnorm_gamma_f32 (cpu/reference/ref_ops.c:196-218) after the
  * residual ADD (adapters/llama/llama.c:746-751, :786-791). One workgroup;
- * each thread keeps its elements in registers between the two passes. */
+ * thread j holds the float4 groups j, j + 256, ... of x, delta and gamma in
+ * registers (all loads issued before the reduction). n % 4 == 0. */
 __global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm(float *__restrict__ x,
                                                               const float *__restrict__ delta,
                                                               const float *__restrict__ gamma,
                                                               float *__restrict__ xn, uint32_t n,
                                                               float eps) {
   __shared__ double sh[kNormThreads / 64];
-  float v[kNormPer];
+  const uint32_t n4 = n >> 2;
+  float4 v[kNormVec], g[kNormVec];
+#pragma unroll
+  for (int j = 0; j < kNormVec; ++j) {
+    const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
+    v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    g[j] = v[j];
+    if (i < n4) {
+      v[j] = reinterpret_cast<const float4 *>(x)[i];
+      g[j] = reinterpret_cast<const float4 *>(gamma)[i];
+    }
+  }
+  if (delta != nullptr) {
+#pragma unroll
+    for (int j = 0; j < kNormVec; ++j) {
+      const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
+      if (i < n4) {
+        const float4 d = reinterpret_cast<const float4 *>(delta)[i];
+        v[j] = make_float4(v[j].x + d.x, v[j].y + d.y, v[j].z + d.z, v[j].w + d.w);
+        reinterpret_cast<float4 *>(x)[i] = v[j];
+      }
+    }
+  }
   double acc = 0.0;
 #pragma unroll
-  for (int j = 0; j < kNormPer; ++j) {
-    const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
-    v[j] = 0.0f;
-    if (i < n) {
-      float t = x[i];
-      if (delta != nullptr) {
-        t = t + delta[i];
-        x[i] = t;
-      }
-      v[j] = t;
-      acc += (double)t * (double)t;
-    }
+  for (int j = 0; j < kNormVec; ++j) {
+    acc += (double)v[j].x * (double)v[j].x;
+    acc += (double)v[j].y * (double)v[j].y;
+    acc += (double)v[j].z * (double)v[j].z;
+    acc += (double)v[j].w * (double)v[j].w;
   }
   const double tot = block_sum(acc, sh);
   const float rms = 1.0f / sqrtf((float)(tot / (double)n) + eps);
 #pragma unroll
-  for (int j = 0; j < kNormPer; ++j) {
+  for (int j = 0; j < kNormVec; ++j) {
     const uint32_t i = threadIdx.x + (uint32_t)j * kNormThreads;
-    if (i < n) xn[i] = v[j] * gamma[i] * rms;
+    if (i < n4)
+      reinterpret_cast<float4 *>(xn)[i] =
+          make_float4(v[j].x * g[j].x * rms, v[j].y * g[j].y * rms, v[j].z * g[j].z * rms,
+                      v[j].w * g[j].w * rms);
   }
+}
+
+/* The same for any n (one element per step), for rows whose length is not
+ * a multiple of 4 or whose pointers are not 16-byte aligned. */
+__global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm_any(float *__restrict__ x,
+                                                                  const float *__restrict__ delta,
+                                                                  const float *__restrict__ gamma,
+                                                                  float *__restrict__ xn,
+                                                                  uint32_t n, float eps) {
+  __shared__ double sh[kNormThreads / 64];
+  double acc = 0.0;
+  for (uint32_t i = threadIdx.x; i < n; i += kNormThreads) {
+    float t = x[i];
+    if (delta != nullptr) {
+      t = t + delta[i];
+      x[i] = t;
+    }
+    acc += (double)t * (double)t;
+  }
+  const double tot = block_sum(acc, sh);
+  const float rms = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += kNormThreads) xn[i] = x[i] * gamma[i] * rms;
 }
 
 /* RoPE at position pos on the heads of q (hq heads) and k (hk heads) of
@@ -114,15 +155,25 @@ __global__ void __launch_bounds__(256) k_rope_append(const float *__restrict__ q
  * (h * hk) / hq), scores are (q . k) / sqrtf(hd), softmax subtracts the
  * maximum, and the output is the probability-weighted sum of v.
  *
+ * With knew set, the kernel first does the step's RoPE and cache append
+ * (k_rope_append's arithmetic): q is rotated on the fly, and the chunk
+ * holding position len - 1 rotates knew, rounds it and vnew to fp16,
+ * stores them at that position and uses its own copies of them.
+ *
  * Split over the context: workgroup (kvh, c) covers positions
  * [64c, 64c + 64) for the G heads of KV head kvh, so each K and V row is
  * read once for all G heads. A wave takes 16 positions; HD/8 lanes share a
  * row (16 bytes of fp16 each: one coalesced 256-byte row read for HD=128).
  * Each wave keeps (max, sum of e^(s-max), sum of e^(s-max) v) per head;
- * the four waves are merged in LDS and the chunk's triple is written to
- * part[(kvh*nch + c)*G + g] = {m, l, o[HD]}. */
+ * the four waves are merged in LDS and the chunk's triple goes to
+ * part[(kvh*nch + c)*G + g] = {m, l, o[HD]}. The last chunk of a KV head
+ * to finish (a device-scope counter per KV head, released and acquired
+ * with fences; nothing waits) merges that head group's chunks in chunk
+ * order, M = max m_c, o = (sum o_c e^(m_c - M)) / (sum l_c e^(m_c - M)),
+ * and resets the counter to zero for the next call. */
 constexpr uint32_t kChunk = 64;
 constexpr uint32_t kMaxG = 8;
+constexpr uint32_t kMaxChunks = 512; /* len <= 32768 */
 
 __device__ __forceinline__ float f16lo(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
@@ -131,36 +182,80 @@ __device__ __forceinline__ float f16hi(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
+/* element i of a RoPE-rotated row (pai_ref_rope_f32's arithmetic) */
+__device__ __forceinline__ float rope_at(const float *__restrict__ src, uint32_t i, uint32_t r2,
+                                         const float *__restrict__ cos_t,
+                                         const float *__restrict__ sin_t) {
+  if (i < r2) return src[i] * cos_t[i] - src[i + r2] * sin_t[i];
+  if (i < 2u * r2) return src[i - r2] * sin_t[i - r2] + src[i] * cos_t[i - r2];
+  return src[i];
+}
+
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
-                                                   const _Float16 *__restrict__ kc,
-                                                   const _Float16 *__restrict__ vc,
-                                                   float *__restrict__ part, uint32_t G,
-                                                   uint32_t ctx, uint32_t len, uint32_t nch) {
+__global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
+                                              const float *__restrict__ knew,
+                                              const float *__restrict__ vnew,
+                                              const float *__restrict__ cos_t,
+                                              const float *__restrict__ sin_t, uint32_t r2,
+                                              _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
+                                              float *__restrict__ part,
+                                              uint32_t *__restrict__ counters,
+                                              float *__restrict__ o, uint32_t G, uint32_t ctx,
+                                              uint32_t len, uint32_t nch) {
   constexpr int LP = HD / 8;   /* lanes per row */
   constexpr int PPI = 64 / LP; /* rows per wave instruction */
   constexpr int IT = 16 / PPI; /* iterations over a wave's 16 rows */
+  __shared__ float qs[kMaxG][HD];
+  __shared__ float nk[HD], nv[HD];
   __shared__ float sm[4][kMaxG], sl[4][kMaxG];
   __shared__ float so[4][kMaxG][HD];
+  __shared__ float fsc[kMaxChunks][kMaxG];
+  __shared__ float sL[kMaxG];
+  __shared__ uint32_t s_last;
   const uint32_t kvh = blockIdx.x / nch, c = blockIdx.x % nch;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t slot = lane / LP, t = lane % LP;
   const float scale = 1.0f / sqrtf((float)HD);
-  const _Float16 *kb = kc + (size_t)kvh * ctx * HD;
-  const _Float16 *vb = vc + (size_t)kvh * ctx * HD;
+  _Float16 *kb = kc + (size_t)kvh * ctx * HD;
+  _Float16 *vb = vc + (size_t)kvh * ctx * HD;
   const uint32_t base = c * kChunk + wave * 16u;
+  const bool append = knew != nullptr;
+  const uint32_t pos = len - 1u;
 
-  /* this lane's rows: 8 K and 8 V values each (fp16 -> f32) */
-  float kr[IT][8], vr[IT][8];
+  /* this lane's rows: 8 K and 8 V values each, loads issued first */
+  uint4 kw[IT], vw[IT];
   bool ok[IT];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const uint32_t p = base + (uint32_t)(it * PPI) + slot;
     ok[it] = p < len;
     const uint32_t pc = ok[it] ? p : 0u; /* an in-bounds row for idle lanes */
-    const uint4 kw = *reinterpret_cast<const uint4 *>(kb + (size_t)pc * HD + 8u * t);
-    const uint4 vw = *reinterpret_cast<const uint4 *>(vb + (size_t)pc * HD + 8u * t);
-    const uint32_t ka[4] = {kw.x, kw.y, kw.z, kw.w}, va[4] = {vw.x, vw.y, vw.z, vw.w};
+    kw[it] = *reinterpret_cast<const uint4 *>(kb + (size_t)pc * HD + 8u * t);
+    vw[it] = *reinterpret_cast<const uint4 *>(vb + (size_t)pc * HD + 8u * t);
+  }
+  /* q of the G heads (rotated when appending) */
+  for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
+    const uint32_t g = e / HD, i = e % HD;
+    const float *src = q + (size_t)(kvh * G + g) * HD;
+    qs[g][i] = append ? rope_at(src, i, r2, cos_t, sin_t) : src[i];
+  }
+  if (append && pos / kChunk == c) {
+    for (uint32_t i = threadIdx.x; i < (uint32_t)HD; i += blockDim.x) {
+      const _Float16 kh = (_Float16)rope_at(knew + (size_t)kvh * HD, i, r2, cos_t, sin_t);
+      const _Float16 vh = (_Float16)vnew[(size_t)kvh * HD + i];
+      kb[(size_t)pos * HD + i] = kh;
+      vb[(size_t)pos * HD + i] = vh;
+      nk[i] = (float)kh;
+      nv[i] = (float)vh;
+    }
+  }
+  __syncthreads();
+
+  float kr[IT][8], vr[IT][8];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const uint32_t ka[4] = {kw[it].x, kw[it].y, kw[it].z, kw[it].w};
+    const uint32_t va[4] = {vw[it].x, vw[it].y, vw[it].z, vw[it].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       kr[it][2 * e] = f16lo(ka[e]);
@@ -168,13 +263,19 @@ __global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
       vr[it][2 * e] = f16lo(va[e]);
       vr[it][2 * e + 1] = f16hi(va[e]);
     }
+    if (append && base + (uint32_t)(it * PPI) + slot == pos) { /* this step's row */
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kr[it][e] = nk[8u * t + e];
+        vr[it][e] = nv[8u * t + e];
+      }
+    }
   }
 
   for (uint32_t g = 0; g < G; ++g) {
-    const float *qh = q + (size_t)(kvh * G + g) * HD + 8u * t;
     float qv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qv[e] = qh[e];
+    for (int e = 0; e < 8; ++e) qv[e] = qs[g][8u * t + e];
     float s[IT];
     float m = -INFINITY;
 #pragma unroll
@@ -183,12 +284,12 @@ __global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
 #pragma unroll
       for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kr[it][e], d);
 #pragma unroll
-      for (int o = LP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+      for (int sh = LP / 2; sh > 0; sh >>= 1) d += __shfl_xor(d, sh, 64);
       s[it] = ok[it] ? d * scale : -INFINITY;
       m = fmaxf(m, s[it]);
     }
 #pragma unroll
-    for (int o = 32; o >= LP; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    for (int sh = 32; sh >= LP; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
     float l = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
@@ -198,10 +299,10 @@ __global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
       for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, vr[it][j], acc[j]);
     }
 #pragma unroll
-    for (int o = 32; o >= LP; o >>= 1) {
-      l += __shfl_xor(l, o, 64);
+    for (int sh = 32; sh >= LP; sh >>= 1) {
+      l += __shfl_xor(l, sh, 64);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += __shfl_xor(acc[j], o, 64);
+      for (int j = 0; j < 8; ++j) acc[j] += __shfl_xor(acc[j], sh, 64);
     }
     if (slot == 0u) {
 #pragma unroll
@@ -214,7 +315,8 @@ __global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
   }
   __syncthreads();
   /* merge the four waves (a wave with no valid row has m = -inf, l = 0) */
-  float *out = part + (size_t)blockIdx.x * G * (HD + 2u);
+  const uint32_t stride = HD + 2u;
+  float *out = part + (size_t)blockIdx.x * G * stride;
   for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
     const uint32_t g = e / HD, d = e % HD;
     float M = -INFINITY;
@@ -225,33 +327,45 @@ __global__ void __launch_bounds__(256) k_attn_part(const float *__restrict__ q,
       L = fmaf(sl[w][g], f, L);
       O = fmaf(so[w][g][d], f, O);
     }
-    out[g * (HD + 2u) + 2u + d] = O;
+    out[g * stride + 2u + d] = O;
     if (d == 0u) {
-      out[g * (HD + 2u)] = M;
-      out[g * (HD + 2u) + 1u] = L;
+      out[g * stride] = M;
+      out[g * stride + 1u] = L;
     }
   }
-}
 
-/* Merge the chunks of each head: M = max m_c, L = sum l_c e^(m_c - M),
- * o = (sum o_c e^(m_c - M)) / L, chunks in order. One workgroup per q head;
- * every chunk holds at least one position, so each m_c is finite. */
-__global__ void __launch_bounds__(256) k_attn_combine(const float *__restrict__ part,
-                                                      float *__restrict__ o, uint32_t G,
-                                                      uint32_t hd, uint32_t nch) {
-  const uint32_t h = blockIdx.x, kvh = h / G, g = h % G;
-  const size_t stride = (size_t)G * (hd + 2u);
-  const float *p0 = part + (size_t)kvh * nch * stride + (size_t)g * (hd + 2u);
-  float M = -INFINITY;
-  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, p0[c * stride]);
-  float L = 0.0f;
-  for (uint32_t c = 0; c < nch; ++c) L = fmaf(p0[c * stride + 1u], expf(p0[c * stride] - M), L);
-  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.0f;
-    for (uint32_t c = 0; c < nch; ++c)
-      acc = fmaf(p0[c * stride + 2u + d], expf(p0[c * stride] - M), acc);
-    o[(size_t)h * hd + d] = acc / L;
+  /* count this chunk; the last of the KV head merges the chunks */
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(&counters[kvh], 1u) == nch - 1u ? 1u : 0u;
+  __syncthreads();
+  if (s_last == 0u) return;
+  __threadfence();
+  const float *pk = part + (size_t)kvh * nch * G * stride;
+  for (uint32_t g = wave; g < G; g += blockDim.x >> 6) {
+    float M = -INFINITY;
+    for (uint32_t cc = lane; cc < nch; cc += 64u) M = fmaxf(M, pk[((size_t)cc * G + g) * stride]);
+    for (int sh = 32; sh > 0; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
+    float L = 0.0f;
+    for (uint32_t cc = lane; cc < nch; cc += 64u) {
+      const float *pc = pk + ((size_t)cc * G + g) * stride;
+      const float f = expf(pc[0] - M);
+      fsc[cc][g] = f;
+      L = fmaf(pc[1], f, L);
+    }
+    for (int sh = 32; sh > 0; sh >>= 1) L += __shfl_xor(L, sh, 64);
+    if (lane == 0u) sL[g] = L;
   }
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
+    const uint32_t g = e / HD, d = e % HD;
+    const float *pc = pk + (size_t)g * stride + 2u + d;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t cc = 0; cc < nch; ++cc) acc = fmaf(pc[(size_t)cc * G * stride], fsc[cc][g], acc);
+    o[(size_t)(kvh * G + g) * HD + d] = acc / sL[g];
+  }
+  if (threadIdx.x == 0) atomicExch(&counters[kvh], 0u);
 }
 
 /* Greedy token: the first index of the largest logit, as the reference's
@@ -342,12 +456,17 @@ __global__ void __launch_bounds__(256) k_dequant_row(paik_qview_t v,
 using namespace paik;
 using namespace paik::dec;
 
-extern "C" uint32_t paik_norm_max(void) { return (uint32_t)(kNormPer * kNormThreads); }
+extern "C" uint32_t paik_norm_max(void) { return (uint32_t)(4 * kNormVec * kNormThreads); }
 
 extern "C" int paik_add_rmsnorm(float *x, const float *delta, const float *gamma, float *xn,
                                 uint32_t n, float eps, void *stream) {
   if (n == 0u || n > paik_norm_max()) return (int)hipErrorInvalidValue;
-  k_add_rmsnorm<<<1, kNormThreads, 0, (hipStream_t)stream>>>(x, delta, gamma, xn, n, eps);
+  const uintptr_t al = (uintptr_t)x | (uintptr_t)delta | (uintptr_t)gamma | (uintptr_t)xn;
+  hipStream_t s = (hipStream_t)stream;
+  if ((n & 3u) == 0u && (al & 15u) == 0u)
+    k_add_rmsnorm<<<1, kNormThreads, 0, s>>>(x, delta, gamma, xn, n, eps);
+  else
+    k_add_rmsnorm_any<<<1, kNormThreads, 0, s>>>(x, delta, gamma, xn, n, eps);
   return (int)hipGetLastError();
 }
 
@@ -364,23 +483,36 @@ extern "C" int paik_rope_append(const float *q, const float *k, const float *v, 
 }
 
 extern "C" uint32_t paik_attn_chunks(uint32_t len) { return (len + kChunk - 1u) / kChunk; }
+extern "C" uint32_t paik_attn_max_len(void) { return kMaxChunks * kChunk; }
 
-extern "C" int paik_attn_decode(const float *q, const void *kc, const void *vc, float *part,
-                                float *o, uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
-                                uint32_t len, void *stream) {
-  if (hk == 0u || hq % hk != 0u || hq / hk > kMaxG || len == 0u || len > ctx)
+extern "C" int paik_attn_decode(const float *q, const float *knew, const float *vnew,
+                                const float *cos_t, const float *sin_t, uint32_t r2, void *kc,
+                                void *vc, float *part, uint32_t *counters, float *o, uint32_t hq,
+                                uint32_t hk, uint32_t hd, uint32_t ctx, uint32_t len,
+                                void *stream) {
+  if (hk == 0u || hq % hk != 0u || hq / hk > kMaxG || len == 0u || len > ctx ||
+      len > paik_attn_max_len())
     return (int)hipErrorInvalidValue;
+  if (knew != nullptr && (r2 == 0u || 2u * r2 > hd)) return (int)hipErrorInvalidValue;
   const uint32_t G = hq / hk, nch = paik_attn_chunks(len);
   hipStream_t s = (hipStream_t)stream;
-  const _Float16 *k16 = static_cast<const _Float16 *>(kc);
-  const _Float16 *v16 = static_cast<const _Float16 *>(vc);
+  _Float16 *k16 = static_cast<_Float16 *>(kc), *v16 = static_cast<_Float16 *>(vc);
   switch (hd) {
-  case 64: k_attn_part<64><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
-  case 128: k_attn_part<128><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
-  case 256: k_attn_part<256><<<hk * nch, 256, 0, s>>>(q, k16, v16, part, G, ctx, len, nch); break;
-  default: return (int)hipErrorInvalidValue;
+  case 64:
+    k_attn<64><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, counters,
+                                        o, G, ctx, len, nch);
+    break;
+  case 128:
+    k_attn<128><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part,
+                                         counters, o, G, ctx, len, nch);
+    break;
+  case 256:
+    k_attn<256><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part,
+                                         counters, o, G, ctx, len, nch);
+    break;
+  default:
+    return (int)hipErrorInvalidValue;
   }
-  k_attn_combine<<<hq, 256, 0, s>>>(part, o, G, hd, nch);
   return (int)hipGetLastError();
 }
 

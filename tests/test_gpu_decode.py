@@ -129,8 +129,8 @@ def test_attention_decode(hq, hk, hd, ctx, lens, qscale):
     vc = f16(rng.standard_normal((hk, ctx, hd)))
     bkc, bvc = dev(kc), dev(vc)
     bo = hm.DeviceBuffer(4 * hq * hd)
-    ws = hm.DeviceBuffer(lib().pai_attention_workspace_bytes(hq, hd, ctx))
-    for length in lens:
+    ws = dev(np.zeros(lib().pai_attention_workspace_bytes(hq, hd, ctx), np.uint8))
+    for length in lens:  # one workspace for all calls: each leaves it reusable
         say(f"[gpu] attention hq={hq} hk={hk} hd={hd} ctx={ctx} len={length} qscale={qscale}")
         q = (rng.standard_normal((hq, hd)) * qscale).astype(np.float32)
         bq = dev(q)
@@ -159,6 +159,48 @@ def attention_f64(q, kc, vc, hq, hk, length):
         pr = np.exp(sc - sc.max())
         out[h] = (pr / pr.sum()) @ V
     return out
+
+
+@pytest.mark.parametrize("hq,hk,hd,r2,pos", [(32, 8, 128, 64, 2047), (32, 8, 128, 64, 64),
+                                         (8, 2, 64, 16, 0), (16, 2, 256, 128, 130)])
+def test_attention_rope_fused_equals_two_ops(hq, hk, hd, r2, pos):
+    """One launch (RoPE + append + attention) gives bit for bit what
+    pai_rope_kv_append_async followed by pai_attention_decode_async gives,
+    in the output and in both caches."""
+    say(f"[gpu] fused rope+attention hq={hq} hk={hk} hd={hd} r2={r2} pos={pos}")
+    ctx = max(pos + 1, 160)
+    rng = np.random.default_rng(pos + hd)
+    kc0 = f16(rng.standard_normal((hk, ctx, hd)))
+    vc0 = f16(rng.standard_normal((hk, ctx, hd)))
+    q = rng.standard_normal((hq, hd)).astype(np.float32)
+    k = rng.standard_normal((hk, hd)).astype(np.float32)
+    v = rng.standard_normal((hk, hd)).astype(np.float32)
+    c, s = ob.rope_tables(ctx, r2, 2 * r2, 500000.0)
+    bq, bk, bv, bc, bs = dev(q), dev(k), dev(v), dev(c), dev(s)
+    row = pos * r2 * 4
+    wsb = lib().pai_attention_workspace_bytes(hq, hd, ctx)
+    outs, caches = [], []
+    for fused in (False, True):
+        bkc, bvc = dev(kc0), dev(vc0)
+        ws = dev(np.zeros(wsb, np.uint8))
+        bo = hm.DeviceBuffer(4 * hq * hd)
+        if fused:
+            check(lib().pai_attention_decode_rope_async(
+                bq.ptr, bk.ptr, bv.ptr, bc.ptr + row, bs.ptr + row, r2, bkc.ptr, bvc.ptr, bo.ptr,
+                ws.ptr, hq, hk, hd, ctx, pos, None), "pai_attention_decode_rope_async")
+        else:
+            bqr = hm.DeviceBuffer(q.nbytes)
+            check(lib().pai_rope_kv_append_async(bq.ptr, bk.ptr, bv.ptr, bqr.ptr, bkc.ptr, bvc.ptr,
+                                                 bc.ptr + row, bs.ptr + row, hq, hk, hd, r2, ctx,
+                                                 pos, None), "pai_rope_kv_append_async")
+            check(lib().pai_attention_decode_async(bqr.ptr, bkc.ptr, bvc.ptr, bo.ptr, ws.ptr, hq,
+                                                   hk, hd, ctx, pos + 1, None),
+                  "pai_attention_decode_async")
+        hm.synchronize()
+        outs.append(bo.download((hq, hd)))
+        caches.append((bkc.download((hk, ctx, hd), np.uint16), bvc.download((hk, ctx, hd), np.uint16)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(caches[0][0], caches[1][0]) and np.array_equal(caches[0][1], caches[1][1])
 
 
 def test_argmax():
