@@ -55,10 +55,9 @@ pai_status_t pai_rope_kv_append_async(const float *q, const float *k, const floa
                                       uint32_t pos, void *stream);
 
 /* Bytes of the workspace the attention calls need for hq heads of
- * dimension hd over len positions. The workspace (256-byte aligned) must be
- * zero-filled before its first use; every call leaves it fit for the next
- * (its per-KV-head counters return to zero). Calls sharing a workspace
- * must not overlap. */
+ * dimension hd over len positions: the per-chunk partial results, which
+ * every call writes before it reads them (no initialisation needed). The
+ * workspace is 256-byte aligned; calls sharing one must not overlap. */
 uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len);
 
 /* Attention of one query position over cache positions 0..len-1:
@@ -66,9 +65,9 @@ uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len);
  * head h reading KV head h / (hq / hk). The last row of
  * pai_ref_attention_f32 (cpu/reference/ref_ops.c:287-340) with keys and
  * values taken from the fp16 caches ([hk][ctx][hd]). hd in {64, 128, 256},
- * hq / hk <= 8, hk <= 256, 1 <= len <= min(ctx, 32768). One launch: the
- * context is split in chunks of 64 positions, and the last chunk of each
- * KV head to finish merges that head group's chunks. The dot products and
+ * hq / hk <= 8, 1 <= len <= min(ctx, 32768). Two launches: the context
+ * is split in chunks of 64 positions (one workgroup per KV head and chunk),
+ * then one workgroup per query head combines its chunks. The dot products and
  * sums run in another order (and with FMA) than the reference's: rel-L2
  * <= 1e-5 against its formula where scores are O(1); for large scores,
  * where the reference's own f32 evaluation errs by as much, within twice
@@ -78,7 +77,7 @@ pai_status_t pai_attention_decode_async(const float *q, const void *k_cache,
                                         uint32_t hq, uint32_t hk, uint32_t hd, uint32_t ctx,
                                         uint32_t len, void *stream);
 
-/* The decode step's attention block in one launch: RoPE of q and k at
+/* The decode step's attention block in the same two launches: RoPE of q and k at
  * position pos (as pai_rope_kv_append_async, bit for bit), the append of
  * the rotated k and of v at pos (fp16), and pai_attention_decode_async over
  * positions 0..pos. q: [hq][hd] and k, v: [hk][hd] as the projections

@@ -72,11 +72,8 @@ pai_status_t pai_rope_kv_append_async(const float *q, const float *k, const floa
   return PAI_OK;
 }
 
-#define ATTN_COUNTER_BYTES 1024u /* one uint32 per KV head, up to 256 */
-
 uint64_t pai_attention_workspace_bytes(uint32_t hq, uint32_t hd, uint32_t len) {
-  return ATTN_COUNTER_BYTES +
-         (uint64_t)hq * paik_attn_chunks(len) * ((uint64_t)hd + 2u) * sizeof(float);
+  return (uint64_t)hq * paik_attn_chunks(len) * ((uint64_t)hd + 2u) * sizeof(float);
 }
 
 static pai_status_t check_attention(const float *q, const void *k_cache, const void *v_cache,
@@ -88,7 +85,6 @@ static pai_status_t check_attention(const float *q, const void *k_cache, const v
     return fail(PAI_ERR_INVALID_ARG, "zero size");
   if (hq % hk != 0u) return fail(PAI_ERR_INVALID_ARG, "hq=%u not a multiple of hk=%u", hq, hk);
   if (hq / hk > 8u) return fail(PAI_ERR_UNSUPPORTED, "hq / hk = %u above 8", hq / hk);
-  if (hk > ATTN_COUNTER_BYTES / 4u) return fail(PAI_ERR_UNSUPPORTED, "hk=%u above 256", hk);
   if (hd != 64u && hd != 128u && hd != 256u)
     return fail(PAI_ERR_UNSUPPORTED, "head size %u (64, 128 or 256)", hd);
   if (len > ctx) return fail(PAI_ERR_INVALID_ARG, "len=%u above ctx=%u", len, ctx);
@@ -105,9 +101,8 @@ pai_status_t pai_attention_decode_async(const float *q, const void *k_cache, con
                                         float *out, void *workspace, uint32_t hq, uint32_t hk,
                                         uint32_t hd, uint32_t ctx, uint32_t len, void *stream) {
   TRY(check_attention(q, k_cache, v_cache, out, workspace, hq, hk, hd, ctx, len));
-  char *ws = (char *)workspace;
   LAUNCH(paik_attn_decode(q, NULL, NULL, NULL, NULL, 0u, (void *)k_cache, (void *)v_cache,
-                          (float *)(ws + ATTN_COUNTER_BYTES), (uint32_t *)ws, out, hq, hk, hd, ctx,
+                          (float *)workspace, out, hq, hk, hd, ctx,
                           len, stream),
          "attention launch");
   return PAI_OK;
@@ -125,9 +120,8 @@ pai_status_t pai_attention_decode_rope_async(const float *q, const float *k, con
   if (r2 == 0u || 2u * r2 > hd)
     return fail(PAI_ERR_UNSUPPORTED, "r2=%u: need 1 <= r2 and 2 r2 <= hd=%u", r2, hd);
   TRY(check_attention(q, k_cache, v_cache, out, workspace, hq, hk, hd, ctx, pos + 1u));
-  char *ws = (char *)workspace;
   LAUNCH(paik_attn_decode(q, k, v, cos_t, sin_t, r2, k_cache, v_cache,
-                          (float *)(ws + ATTN_COUNTER_BYTES), (uint32_t *)ws, out, hq, hk, hd, ctx,
+                          (float *)workspace, out, hq, hk, hd, ctx,
                           pos + 1u, stream),
          "attention launch");
   return PAI_OK;

@@ -90,13 +90,13 @@ int paik_rope_append(const float *q, const float *k, const float *v, float *qo,
 /* Attention over cache positions [0, len). With knew/vnew set, RoPE of q
  * and knew (tables of position len - 1) and the append of knew, vnew at
  * position len - 1 happen in the same launch. part holds
- * hq * paik_attn_chunks(len) * (hd + 2) floats; counters holds hk zeros
- * (left zero by every call). len <= paik_attn_max_len(). */
+ * hq * paik_attn_chunks(len) * (hd + 2) floats (the per-chunk partials,
+ * combined by a second launch). len <= paik_attn_max_len(). */
 uint32_t paik_attn_chunks(uint32_t len);
 uint32_t paik_attn_max_len(void);
 int paik_attn_decode(const float *q, const float *knew, const float *vnew,
                      const float *cos_t, const float *sin_t, uint32_t r2, void *kc,
-                     void *vc, float *part, uint32_t *counters, float *o, uint32_t hq,
+                     void *vc, float *part, float *o, uint32_t hq,
                      uint32_t hk, uint32_t hd, uint32_t ctx, uint32_t len, void *stream);
 /* pv, pi hold paik_argmax_parts() entries */
 uint32_t paik_argmax_parts(void);

@@ -166,11 +166,12 @@ __global__ void __launch_bounds__(256) k_rope_append(const float *__restrict__ q
  * row (16 bytes of fp16 each: one coalesced 256-byte row read for HD=128).
  * Each wave keeps (max, sum of e^(s-max), sum of e^(s-max) v) per head;
  * the four waves are merged in LDS and the chunk's triple goes to
- * part[(kvh*nch + c)*G + g] = {m, l, o[HD]}. The last chunk of a KV head
- * to finish (a device-scope counter per KV head, released and acquired
- * with fences; nothing waits) merges that head group's chunks in chunk
- * order, M = max m_c, o = (sum o_c e^(m_c - M)) / (sum l_c e^(m_c - M)),
- * and resets the counter to zero for the next call. */
+ * part[(kvh*nch + c)*G + g] = {m, l, o[HD]}. k_attn_merge, the next
+ * launch, combines the chunks of each head in chunk order:
+ * M = max m_c, o = (sum o_c e^(m_c - M)) / (sum l_c e^(m_c - M)).
+ * (A single launch whose last chunk merges needs a device-scope release and
+ * acquire per workgroup; across the chip's separate L2 caches that cost
+ * about 30 us per call at 264 workgroups, against a few for a launch.) */
 constexpr uint32_t kChunk = 64;
 constexpr uint32_t kMaxG = 8;
 constexpr uint32_t kMaxChunks = 512; /* len <= 32768 */
@@ -198,10 +199,8 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
                                               const float *__restrict__ cos_t,
                                               const float *__restrict__ sin_t, uint32_t r2,
                                               _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
-                                              float *__restrict__ part,
-                                              uint32_t *__restrict__ counters,
-                                              float *__restrict__ o, uint32_t G, uint32_t ctx,
-                                              uint32_t len, uint32_t nch) {
+                                              float *__restrict__ part, uint32_t G,
+                                              uint32_t ctx, uint32_t len, uint32_t nch) {
   constexpr int LP = HD / 8;   /* lanes per row */
   constexpr int PPI = 64 / LP; /* rows per wave instruction */
   constexpr int IT = 16 / PPI; /* iterations over a wave's 16 rows */
@@ -209,9 +208,6 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
   __shared__ float nk[HD], nv[HD];
   __shared__ float sm[4][kMaxG], sl[4][kMaxG];
   __shared__ float so[4][kMaxG][HD];
-  __shared__ float fsc[kMaxChunks][kMaxG];
-  __shared__ float sL[kMaxG];
-  __shared__ uint32_t s_last;
   const uint32_t kvh = blockIdx.x / nch, c = blockIdx.x % nch;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t slot = lane / LP, t = lane % LP;
@@ -334,38 +330,57 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
     }
   }
 
-  /* count this chunk; the last of the KV head merges the chunks */
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&counters[kvh], 1u) == nch - 1u ? 1u : 0u;
-  __syncthreads();
-  if (s_last == 0u) return;
-  __threadfence();
-  const float *pk = part + (size_t)kvh * nch * G * stride;
-  for (uint32_t g = wave; g < G; g += blockDim.x >> 6) {
+}
+
+/* The chunks' triples of one head combined in chunk order (see k_attn):
+ * workgroup h is query head h, thread d output element d. */
+template <int HD>
+__global__ void __launch_bounds__(HD) k_attn_merge(const float *__restrict__ part,
+                                                   float *__restrict__ o, uint32_t G,
+                                                   uint32_t nch) {
+  constexpr uint32_t stride = HD + 2u;
+  constexpr int PER = kMaxChunks / 64; /* chunks per lane of the first wave */
+  __shared__ float fsc[kMaxChunks];
+  __shared__ float sL;
+  const uint32_t h = blockIdx.x, kvh = h / G, g = h % G;
+  const size_t cstep = (size_t)G * stride; /* floats from one chunk's triple to the next */
+  const float *pk = part + ((size_t)kvh * nch * G + g) * stride;
+  if (threadIdx.x < 64u) {
+    const uint32_t lane = threadIdx.x;
+    float mv[PER], lv[PER];
     float M = -INFINITY;
-    for (uint32_t cc = lane; cc < nch; cc += 64u) M = fmaxf(M, pk[((size_t)cc * G + g) * stride]);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const uint32_t cc = lane + 64u * (uint32_t)j;
+      mv[j] = -INFINITY;
+      lv[j] = 0.0f;
+      if (cc < nch) {
+        mv[j] = pk[cc * cstep];
+        lv[j] = pk[cc * cstep + 1u];
+      }
+      M = fmaxf(M, mv[j]);
+    }
     for (int sh = 32; sh > 0; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
     float L = 0.0f;
-    for (uint32_t cc = lane; cc < nch; cc += 64u) {
-      const float *pc = pk + ((size_t)cc * G + g) * stride;
-      const float f = expf(pc[0] - M);
-      fsc[cc][g] = f;
-      L = fmaf(pc[1], f, L);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const uint32_t cc = lane + 64u * (uint32_t)j;
+      if (cc < nch) {
+        const float f = expf(mv[j] - M);
+        fsc[cc] = f;
+        L = fmaf(lv[j], f, L);
+      }
     }
     for (int sh = 32; sh > 0; sh >>= 1) L += __shfl_xor(L, sh, 64);
-    if (lane == 0u) sL[g] = L;
+    if (lane == 0u) sL = L;
   }
   __syncthreads();
-  for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
-    const uint32_t g = e / HD, d = e % HD;
-    const float *pc = pk + (size_t)g * stride + 2u + d;
-    float acc = 0.0f;
+  const uint32_t d = threadIdx.x;
+  const float *pc = pk + 2u + d;
+  float acc = 0.0f;
 #pragma unroll 8
-    for (uint32_t cc = 0; cc < nch; ++cc) acc = fmaf(pc[(size_t)cc * G * stride], fsc[cc][g], acc);
-    o[(size_t)(kvh * G + g) * HD + d] = acc / sL[g];
-  }
-  if (threadIdx.x == 0) atomicExch(&counters[kvh], 0u);
+  for (uint32_t cc = 0; cc < nch; ++cc) acc = fmaf(pc[cc * cstep], fsc[cc], acc);
+  o[(size_t)h * HD + d] = acc / sL;
 }
 
 /* Greedy token: the first index of the largest logit, as the reference's
@@ -487,9 +502,8 @@ extern "C" uint32_t paik_attn_max_len(void) { return kMaxChunks * kChunk; }
 
 extern "C" int paik_attn_decode(const float *q, const float *knew, const float *vnew,
                                 const float *cos_t, const float *sin_t, uint32_t r2, void *kc,
-                                void *vc, float *part, uint32_t *counters, float *o, uint32_t hq,
-                                uint32_t hk, uint32_t hd, uint32_t ctx, uint32_t len,
-                                void *stream) {
+                                void *vc, float *part, float *o, uint32_t hq, uint32_t hk,
+                                uint32_t hd, uint32_t ctx, uint32_t len, void *stream) {
   if (hk == 0u || hq % hk != 0u || hq / hk > kMaxG || len == 0u || len > ctx ||
       len > paik_attn_max_len())
     return (int)hipErrorInvalidValue;
@@ -499,16 +513,19 @@ extern "C" int paik_attn_decode(const float *q, const float *knew, const float *
   _Float16 *k16 = static_cast<_Float16 *>(kc), *v16 = static_cast<_Float16 *>(vc);
   switch (hd) {
   case 64:
-    k_attn<64><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, counters,
-                                        o, G, ctx, len, nch);
+    k_attn<64><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
+                                        len, nch);
+    k_attn_merge<64><<<hq, 64, 0, s>>>(part, o, G, nch);
     break;
   case 128:
-    k_attn<128><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part,
-                                         counters, o, G, ctx, len, nch);
+    k_attn<128><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
+                                         len, nch);
+    k_attn_merge<128><<<hq, 128, 0, s>>>(part, o, G, nch);
     break;
   case 256:
-    k_attn<256><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part,
-                                         counters, o, G, ctx, len, nch);
+    k_attn<256><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
+                                         len, nch);
+    k_attn_merge<256><<<hq, 256, 0, s>>>(part, o, G, nch);
     break;
   default:
     return (int)hipErrorInvalidValue;

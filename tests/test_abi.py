@@ -155,7 +155,7 @@ def test_decode_entry_points_reject_bad_arguments_before_device():
     assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 0, 0.0, None) == -1
     assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 16385, 0.0, None) == -3
     assert lib.pai_argmax_f32_async(fake, 0, fake, fake, None) == -1
-    assert lib.pai_attention_workspace_bytes(32, 128, 2048) == 1024 + 32 * 32 * 130 * 4
+    assert lib.pai_attention_workspace_bytes(32, 128, 2048) == 32 * 32 * 130 * 4
     # the fused RoPE + append + attention: position outside the cache, long contexts
     args = [fake] * 5 + [64] + [fake] * 4
     assert lib.pai_attention_decode_rope_async(*args, 8, 2, 128, 64, 64, None) == -1
