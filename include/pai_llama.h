@@ -40,6 +40,35 @@ extern "C" {
 pai_status_t pai_rmsnorm_f32_async(float *x, const float *delta, const float *gamma,
                                    float *xn, uint64_t n, float eps, void *stream);
 
+/* One-token projections with the decode step's neighbouring operators
+ * fused in, each one launch of the packed GEMV (device pointers, matrices
+ * of pai_qmat_upload). They produce what the reference's op sequence
+ * produces: RMSNORM then GEMM (adapters/llama/llama.c:674-693, :756-769,
+ * :884-891), GEMM then ADD (:742-749, :788-795).
+ *
+ * ys[i] = rmsnorm(x, gamma, eps) W_i^T for count (1..4) matrices of one
+ * format and K (q, k, v; the output head). Each workgroup computes the
+ * RMS of the whole row itself (sum of squares in double, products in the
+ * reference's order, as pai_rmsnorm_f32_async), so no normalised copy of x
+ * is written. K <= 16384 (8192 for Q8_0: one column slice); x and gamma 16-byte aligned,
+ * eps = 0 meaning 1e-5. */
+pai_status_t pai_qgemv_rmsnorm_f32_async(const pai_qmat_t *const *ws, uint32_t count,
+                                         const float *x, const float *gamma, float eps,
+                                         float *const *ys, void *stream);
+
+/* h = silu(xn W_gate^T) * (xn W_up^T) with xn = rmsnorm(x, gamma, eps):
+ * the feed-forward block's norm, gate, up and SiLU-multiply
+ * (adapters/llama/llama.c:756-781) in one launch. Limits as above. */
+pai_status_t pai_qgemv_rmsnorm_gate_up_async(const pai_qmat_t *w_gate, const pai_qmat_t *w_up,
+                                             const float *x, const float *gamma, float eps,
+                                             float *h, void *stream);
+
+/* y += x W^T for one token: the residual ADD after the attention output
+ * and down projections. Each y[j] receives one f32 add of the finished
+ * dot product (x + delta rounds once, as the reference's ADD). */
+pai_status_t pai_qgemv_add_f32_async(const pai_qmat_t *w, const float *x, float *y,
+                                     void *stream);
+
 /* RoPE of one position followed by the KV-cache append. q holds hq heads
  * and k, v hold hk heads of hd floats; each head's pairs (i, i + r2),
  * i < r2, are rotated by the tables cos_t[i], sin_t[i] of position pos:

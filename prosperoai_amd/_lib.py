@@ -55,6 +55,9 @@ SIGNATURES = {
     "pai_hip_op_name": (C.c_char_p, [C.c_uint32]),
     # pai_llama.h
     "pai_rmsnorm_f32_async": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_uint64, C.c_float, _vp]),
+    "pai_qgemv_rmsnorm_f32_async": (C.c_int32, [_vp, C.c_uint32, _vp, _vp, C.c_float, _vp, _vp]),
+    "pai_qgemv_rmsnorm_gate_up_async": (C.c_int32, [_vp, _vp, _vp, _vp, C.c_float, _vp, _vp]),
+    "pai_qgemv_add_f32_async": (C.c_int32, [_vp, _vp, _vp, _vp]),
     "pai_rope_kv_append_async": (C.c_int32, [_vp] * 8 + [C.c_uint32] * 6 + [_vp]),
     "pai_attention_workspace_bytes": (C.c_uint64, [C.c_uint32] * 3),
     "pai_attention_decode_async": (C.c_int32, [_vp] * 5 + [C.c_uint32] * 5 + [_vp]),

@@ -52,6 +52,70 @@ pai_status_t pai_rmsnorm_f32_async(float *x, const float *delta, const float *ga
   return PAI_OK;
 }
 
+/* The one-token projections of the decode step with their neighbours
+ * fused in (paik_gemv_one): the RMSNorm before a projection, the residual
+ * ADD after one. */
+#define PAI_FUSED_MAX 4u
+
+static pai_status_t check_one(const pai_qmat_t *const *ws, uint32_t count, const float *x,
+                              float *const *ys, const paik_qview_t **vs) {
+  if (ws == NULL || ys == NULL || x == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  if (count == 0u || count > PAI_FUSED_MAX)
+    return fail(PAI_ERR_INVALID_ARG, "count=%u, expected 1..%u", count, PAI_FUSED_MAX);
+  for (uint32_t i = 0; i < count; ++i) {
+    if (ws[i] == NULL || ys[i] == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+    vs[i] = pai__qmat_view(ws[i]);
+    if (vs[i]->type != vs[0]->type || vs[i]->k != vs[0]->k)
+      return fail(PAI_ERR_MISMATCH, "matrix %u differs from matrix 0 in type or K", i);
+    if (((uintptr_t)ys[i] & 3u) != 0u) return fail(PAI_ERR_INVALID_ARG, "y must be 4-byte aligned");
+  }
+  if (((uintptr_t)x & 15u) != 0u) return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned");
+  return pai__ready();
+}
+
+static pai_status_t check_gamma(const float *gamma, uint32_t type, uint32_t k) {
+  if (gamma == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  if (((uintptr_t)gamma & 15u) != 0u)
+    return fail(PAI_ERR_INVALID_ARG, "gamma must be 16-byte aligned");
+  if (k > paik_gemv_norm_max_k(type))
+    return fail(PAI_ERR_UNSUPPORTED, "K=%u above %u for the fused RMSNorm", k,
+                paik_gemv_norm_max_k(type));
+  return PAI_OK;
+}
+
+pai_status_t pai_qgemv_rmsnorm_f32_async(const pai_qmat_t *const *ws, uint32_t count,
+                                         const float *x, const float *gamma, float eps,
+                                         float *const *ys, void *stream) {
+  const paik_qview_t *vs[PAI_FUSED_MAX];
+  TRY(check_one(ws, count, x, ys, vs));
+  TRY(check_gamma(gamma, vs[0]->type, vs[0]->k));
+  if (eps == 0.0f) eps = 1e-5f; /* cpu/reference/ref_ops.c:203-205 */
+  LAUNCH(paik_gemv_one(vs, ys, count, 0, x, gamma, eps, 0, stream), "kernel launch");
+  return PAI_OK;
+}
+
+pai_status_t pai_qgemv_rmsnorm_gate_up_async(const pai_qmat_t *w_gate, const pai_qmat_t *w_up,
+                                             const float *x, const float *gamma, float eps,
+                                             float *h, void *stream) {
+  const pai_qmat_t *ws[2] = {w_gate, w_up};
+  float *ys[2] = {h, h};
+  const paik_qview_t *vs[PAI_FUSED_MAX];
+  TRY(check_one(ws, 2u, x, ys, vs));
+  if (vs[0]->n != vs[1]->n) return fail(PAI_ERR_MISMATCH, "gate and up differ in shape");
+  TRY(check_gamma(gamma, vs[0]->type, vs[0]->k));
+  if (eps == 0.0f) eps = 1e-5f;
+  LAUNCH(paik_gemv_one(vs, ys, 2u, 1, x, gamma, eps, 0, stream), "kernel launch");
+  return PAI_OK;
+}
+
+pai_status_t pai_qgemv_add_f32_async(const pai_qmat_t *w, const float *x, float *y,
+                                     void *stream) {
+  const paik_qview_t *vs[PAI_FUSED_MAX];
+  TRY(check_one(&w, 1u, x, &y, vs));
+  LAUNCH(paik_gemv_one(vs, &y, 1u, 0, x, NULL, 0.0f, 1, stream), "kernel launch");
+  return PAI_OK;
+}
+
 pai_status_t pai_rope_kv_append_async(const float *q, const float *k, const float *v,
                                       float *q_out, void *k_cache, void *v_cache,
                                       const float *cos_t, const float *sin_t, uint32_t hq,
@@ -414,39 +478,44 @@ pai_status_t pai_llama_decode_async(pai_llama_t *m, const uint32_t *token_dev, u
   TRY(pai__ready());
   const pai_llama_config_t *c = &m->c;
   const uint32_t E = c->n_embd, hq = c->n_head, hk = c->n_head_kv, hd = m->hd;
-  const uint32_t f = PAI_QGEMM_DEVICE_PTRS;
   const float eps = c->norm_eps;
 
   /* one-hot embedding row (adapters/llama/llama.c:511-520) */
   LAUNCH(paik_dequant_row(pai__qmat_view(m->embd), token_dev, m->x, stream), "embedding launch");
+  /* The residual x is updated in place by the o and down projections
+   * (x += W a), and each RMSNorm runs inside the projection that consumes
+   * it, so a layer is five launches. */
   for (uint32_t l = 0; l < c->n_layer; ++l) {
     const pai_qmat_t *const *w = m->w + (size_t)l * W_PER_LAYER;
-    /* x += down(previous layer); xn = rmsnorm(x, attn_norm) */
-    TRY(pai_rmsnorm_f32_async(m->x, l == 0u ? NULL : m->d, m->norms + (size_t)l * E, m->xn, E, eps,
-                              stream));
+    const float *attn_norm = m->norms + (size_t)l * E;
+    const float *ffn_norm = m->norms + ((size_t)c->n_layer + l) * E;
+    /* q, k, v = rmsnorm(x, attn_norm) W^T */
     if (m->fuse_qkv[l]) {
       float *ys[3] = {m->q, m->k, m->v};
-      TRY(pai_qgemm_f32_multi_async(w + W_Q, 3, 1, m->xn, ys, f, stream));
+      TRY(pai_qgemv_rmsnorm_f32_async(w + W_Q, 3, m->x, attn_norm, eps, ys, stream));
     } else {
-      TRY(pai_qgemm_f32_async(w[W_Q], 1, m->xn, m->q, f, stream));
-      TRY(pai_qgemm_f32_async(w[W_K], 1, m->xn, m->k, f, stream));
-      TRY(pai_qgemm_f32_async(w[W_V], 1, m->xn, m->v, f, stream));
+      for (int i = 0; i < 3; ++i) {
+        float *y = i == 0 ? m->q : i == 1 ? m->k : m->v;
+        TRY(pai_qgemv_rmsnorm_f32_async(w + W_Q + i, 1, m->x, attn_norm, eps, &y, stream));
+      }
     }
     uint16_t *kc = cache_of(m, l, 0), *vc = cache_of(m, l, 1);
-    /* RoPE, cache append and attention in one launch */
+    /* RoPE, cache append and attention */
     TRY(pai_attention_decode_rope_async(m->q, m->k, m->v, m->cos_t + (size_t)pos * m->r2,
                                         m->sin_t + (size_t)pos * m->r2, m->r2, kc, vc, m->a,
                                         m->attn_ws, hq, hk, hd, c->ctx, pos, stream));
-    TRY(pai_qgemm_f32_async(w[W_O], 1, m->a, m->o, f, stream));
-    /* x += o; xn = rmsnorm(x, ffn_norm) */
-    TRY(pai_rmsnorm_f32_async(m->x, m->o, m->norms + ((size_t)c->n_layer + l) * E, m->xn, E, eps,
-                              stream));
-    TRY(pai_qgemm_f32_gate_up_async(w[W_GATE], w[W_UP], 1, m->xn, m->h, f, stream));
-    TRY(pai_qgemm_f32_async(w[W_DOWN], 1, m->h, m->d, f, stream));
+    /* x += a W_o^T */
+    TRY(pai_qgemv_add_f32_async(w[W_O], m->a, m->x, stream));
+    /* h = silu(xn W_gate^T) * (xn W_up^T), xn = rmsnorm(x, ffn_norm) */
+    TRY(pai_qgemv_rmsnorm_gate_up_async(w[W_GATE], w[W_UP], m->x, ffn_norm, eps, m->h, stream));
+    /* x += h W_down^T */
+    TRY(pai_qgemv_add_f32_async(w[W_DOWN], m->h, m->x, stream));
   }
-  TRY(pai_rmsnorm_f32_async(m->x, m->d, m->norms + 2u * (size_t)c->n_layer * E, m->xn, E, eps,
-                            stream));
-  TRY(pai_qgemm_f32_async(m->out, 1, m->xn, m->logits, f, stream));
+  {
+    float *y = m->logits;
+    TRY(pai_qgemv_rmsnorm_f32_async(&m->out, 1, m->x, m->norms + 2u * (size_t)c->n_layer * E, eps,
+                                    &y, stream));
+  }
   TRY(pai_argmax_f32_async(m->logits, c->vocab, next_dev, m->arg_ws, stream));
   return PAI_OK;
 }

@@ -69,6 +69,16 @@ int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys,
 int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
                        uint32_t m, const float *x, float *h, void *stream);
 uint32_t paik_gemv_pair_max_k(void);
+/* One token on the integer-dot kernel with the decode step's fusions, in
+ * one launch: y_i = x' W_i^T for count (1..4) matrices of one format and K,
+ * where x' = rmsnorm(x, gamma, eps) when gamma is set (one RMS per
+ * workgroup; K up to paik_gemv_norm_max_k(type)) and x' = x otherwise; accum
+ * set adds the products to y (each output has one writer per launch);
+ * pair set takes vs = {gate, up} (count 2, no accum) and writes
+ * ys[0] = silu(x' W_gate^T) * (x' W_up^T). x and gamma 16-byte aligned. */
+uint32_t paik_gemv_norm_max_k(uint32_t type);
+int paik_gemv_one(const paik_qview_t *const *vs, float *const *ys, uint32_t count, int pair,
+                  const float *x, const float *gamma, float eps, int accum, void *stream);
 /* Batched GEMV on the i8 matrix cores (qgemv_mx.hip): y_i = x W_i^T for
  * count (1..4) matrices of one format and K, or h = silu(x Wg^T) * (x Wu^T),
  * for m tokens in launches of paik_gemv_mx_tokens(k, m) tokens (1, 2, 4

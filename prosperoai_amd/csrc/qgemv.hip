@@ -142,16 +142,24 @@ __device__ __forceinline__ void plane_words(const float v[8], uint32_t jw, XSlot
  * covers up to kXIt * 1024 / 4 = 1024 chunk-tokens (more than the LDS
  * budget holds). */
 constexpr int kXIt = 4;
-/* chunk-tokens one pass of the plane builder covers, per workgroup size */
-__host__ __device__ constexpr uint32_t max_slice_tok(int nw) { return (uint32_t)kXIt * 64u * (uint32_t)nw / 4u; }
+/* The fused-RMSNorm kernels also hold gamma in registers; with 2 passes
+ * (1 for Q8_0, whose codes take twice the registers) they fit the plain
+ * kernels' register budget without spills. */
+template <class F> constexpr int kXItNorm = 2;
+template <> constexpr int kXItNorm<Q8_0> = 1;
+/* chunk-tokens one pass of the plane builder covers, per workgroup size
+ * and passes per thread */
+__host__ __device__ constexpr uint32_t max_slice_tok(int nw, int xi = kXIt) {
+  return (uint32_t)xi * 64u * (uint32_t)nw / 4u;
+}
 
-template <int MT>
+template <int MT, int XI>
 __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, uint32_t ntok,
-                                       uint32_t cs, uint32_t nsc, float4 (&va)[kXIt],
-                                       float4 (&vb)[kXIt]) {
+                                       uint32_t cs, uint32_t nsc, float4 (&va)[XI],
+                                       float4 (&vb)[XI]) {
   const uint32_t total = (uint32_t)MT * nsc * 4u;
 #pragma unroll
-  for (int it = 0; it < kXIt; ++it) {
+  for (int it = 0; it < XI; ++it) {
     const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
     const uint32_t t = idx / (nsc * 4u), r = idx % (nsc * 4u);
     /* Idle threads and tokens >= ntok load nothing (zeros). Given a
@@ -171,12 +179,12 @@ __device__ __forceinline__ void x_load(const float *__restrict__ x, uint32_t k, 
   }
 }
 
-template <int MT>
-__device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[kXIt],
-                                         const float4 (&vb)[kXIt], XSlot *xp, XScale *xf) {
+template <int MT, int XI>
+__device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[XI],
+                                         const float4 (&vb)[XI], XSlot *xp, XScale *xf) {
   const uint32_t total = (uint32_t)MT * nsc * 4u;
 #pragma unroll
-  for (int it = 0; it < kXIt; ++it) {
+  for (int it = 0; it < XI; ++it) {
     const uint32_t idx = threadIdx.x + (uint32_t)it * blockDim.x;
     if (idx < total) { /* whole quads are in or out together */
       const uint32_t t = idx / (nsc * 4u), r = idx % (nsc * 4u);
@@ -200,7 +208,50 @@ struct GemvArgs {
   float *y[kMaxMats];
   uint32_t wave_end[kMaxMats];
   uint32_t count;
+  uint32_t accum;      /* add to y instead of storing (every slice) */
+  const float *gamma;  /* NORM kernels: the RMSNorm weights, K floats */
+  float eps;           /* NORM kernels: RMSNorm epsilon */
 };
+
+/* RMSNorm of a one-token activation row held in registers (the x_load
+ * layout, every element of the row loaded once across the workgroup):
+ * rms = 1 / sqrtf((float)(sum x^2 / n) + eps) with the sum of squares in
+ * double, then x = x * gamma * rms, the two products in that order
+ * (pai_ref_rmsnorm_gamma_f32, cpu/reference/ref_ops.c:195-216). The double
+ * sum runs lanes -> waves in a fixed order. */
+template <int NW, int XI>
+__device__ __forceinline__ void rms_apply(float4 (&va)[XI], float4 (&vb)[XI],
+                                          const float4 (&ga)[XI], const float4 (&gb)[XI],
+                                          uint32_t n, float eps) {
+  __shared__ double red[NW];
+  double acc = 0.0;
+#pragma unroll
+  for (int it = 0; it < XI; ++it) {
+    acc += (double)va[it].x * (double)va[it].x;
+    acc += (double)va[it].y * (double)va[it].y;
+    acc += (double)va[it].z * (double)va[it].z;
+    acc += (double)va[it].w * (double)va[it].w;
+    acc += (double)vb[it].x * (double)vb[it].x;
+    acc += (double)vb[it].y * (double)vb[it].y;
+    acc += (double)vb[it].z * (double)vb[it].z;
+    acc += (double)vb[it].w * (double)vb[it].w;
+  }
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += red[w];
+  const float rms = 1.0f / sqrtf((float)(tot / (double)n) + eps);
+  auto sc = [rms](float4 x, float4 g) {
+    return make_float4(x.x * g.x * rms, x.y * g.y * rms, x.z * g.z * rms, x.w * g.w * rms);
+  };
+#pragma unroll
+  for (int it = 0; it < XI; ++it) {
+    va[it] = sc(va[it], ga[it]);
+    vb[it] = sc(vb[it], gb[it]);
+  }
+}
 
 /* Weight loads of a block are issued for all its lanes and rows with
  * addresses clamped into the matrix (lanes or rows past the end re-read
@@ -211,11 +262,12 @@ struct GemvArgs {
  * add with a non-returning atomic (each output has one writer per launch,
  * and launches on a stream run in order, so the result is the same as a
  * read-add-write). */
-template <class F, int U, int MT, bool PAIR, int NW>
+template <class F, int U, int MT, bool PAIR, int NW, bool NORM>
 __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__restrict__ x,
                                                       uint32_t ntok, uint32_t cs, uint32_t nsc,
                                                       int accumulate) {
   static_assert(U * MT <= 16, "at most 16 outputs per row group");
+  static_assert(!NORM || MT == 1, "the fused RMSNorm takes one token");
   static_assert(!PAIR || U % 2 == 0, "a paired row group holds gate and up rows");
   /* output rows per row group; in a paired launch slot u of a group holds
    * row u/2 of matrix u%2 */
@@ -279,8 +331,11 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
   /* Activation loads first, then the ring of PD blocks (kInFlight
    * row-chunks per lane); the planes are built while the ring is in
    * flight. */
-  float4 xa[kXIt], xb[kXIt];
-  x_load<MT>(x, v.k, ntok, cs, nsc, xa, xb);
+  constexpr int XI = NORM ? kXItNorm<F> : kXIt;
+  float4 xa[XI], xb[XI];
+  x_load<MT, XI>(x, v.k, ntok, cs, nsc, xa, xb);
+  float4 ga[XI], gb[XI]; /* NORM: gamma in the same layout (one slice covers the row) */
+  if constexpr (NORM) x_load<1, XI>(a.gamma, v.k, 1u, cs, nsc, ga, gb);
   constexpr int PD = kInFlight / U;
   typename F::Raw buf[PD][U];
   /* Every load below is unconditional (blocks past the wave's last one
@@ -291,7 +346,8 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 #pragma unroll
   for (int p = 0; p < PD; ++p) load_block((uint32_t)p, buf[p]);
 
-  x_planes<MT>(nsc, xa, xb, xp, xf);
+  if constexpr (NORM) rms_apply<NW, XI>(xa, xb, ga, gb, v.k, a.eps);
+  x_planes<MT, XI>(nsc, xa, xb, xp, xf);
   __syncthreads();
 
   float acc[U][MT];
@@ -430,9 +486,9 @@ static void split_waves(GemvArgs &a, uint32_t total_waves) {
 
 /* Chunks of one column slice: those whose activation planes for MT
  * tokens fit the LDS budget and one pass of the plane builder. */
-static uint32_t slice_cap(uint32_t mt, int nw = kWaves) {
+static uint32_t slice_cap(uint32_t mt, int nw = kWaves, int xi = kXIt) {
   const uint32_t fit = (uint32_t)(kLdsBudget / ((size_t)mt * (sizeof(XSlot) + sizeof(XScale))));
-  return min(fit, max_slice_tok(nw) / mt);
+  return min(fit, max_slice_tok(nw, xi) / mt);
 }
 
 /* One-token launches of up to 4096 rows (two rows per wave on 256
@@ -440,51 +496,52 @@ static uint32_t slice_cap(uint32_t mt, int nw = kWaves) {
  * workgroups, so every CU shares the dot-product work, when a row still
  * fits one column slice of the smaller plane builder (PAI_GEMV_NW=16 / 8
  * forces either). */
-static bool small_wg(uint32_t rows, uint32_t k) {
+static bool small_wg(uint32_t rows, uint32_t k, int xi = kXIt) {
   static const int nw = getenv("PAI_GEMV_NW") ? atoi(getenv("PAI_GEMV_NW")) : 0;
-  if ((k >> 5) > slice_cap(1u, kWavesSmall)) return false; /* rows stay one slice */
+  if ((k >> 5) > slice_cap(1u, kWavesSmall, xi)) return false; /* rows stay one slice */
   if (nw == 16) return false;
   if (nw == 8) return true;
   return rows <= kWavesSmall * 2u * 256u;
 }
 
-template <class F, int U, int MT, bool PAIR, int NW = kWaves>
+template <class F, int U, int MT, bool PAIR, int NW = kWaves, bool NORM = false>
 static hipError_t launch_u(GemvArgs a, const float *x, uint32_t ntok, uint32_t grid,
                            hipStream_t s) {
   const uint32_t nchunks = a.v[0].k >> 5;
-  const uint32_t cap = slice_cap((uint32_t)MT, NW);
+  const uint32_t cap = slice_cap((uint32_t)MT, NW, NORM ? kXItNorm<F> : kXIt);
   const uint32_t slice = cap >= nchunks ? nchunks : (cap & ~63u);
-  if (PAIR && slice != nchunks) return hipErrorInvalidValue; /* the epilogue needs whole rows */
+  /* the silu epilogue and the fused RMSNorm need whole rows */
+  if ((PAIR || NORM) && slice != nchunks) return hipErrorInvalidValue;
   if constexpr (PAIR) a.wave_end[0] = grid * (uint32_t)NW;
   else split_waves(a, grid * (uint32_t)NW);
   for (uint32_t cs = 0; cs < nchunks; cs += slice) {
     const uint32_t nsc = min(slice, nchunks - cs);
     const size_t lds = (size_t)MT * nsc * (sizeof(XSlot) + sizeof(XScale));
-    k_gemv<F, U, MT, PAIR, NW><<<dim3(grid), dim3(64u * NW), lds, s>>>(a, x, ntok, cs, nsc,
-                                                                       cs != 0u ? 1 : 0);
+    k_gemv<F, U, MT, PAIR, NW, NORM><<<dim3(grid), dim3(64u * NW), lds, s>>>(
+        a, x, ntok, cs, nsc, (a.accum != 0u || cs != 0u) ? 1 : 0);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
 
-template <class F, int MT>
+template <class F, int MT, bool NORM = false>
 static hipError_t launch_gemv(const GemvArgs &a, const float *x, uint32_t ntok, hipStream_t s) {
   uint32_t rows = 0;
   for (uint32_t i = 0; i < a.count; ++i) rows += a.v[i].n;
   const uint32_t grid = pick_grid(rows, a.count);
   const int u = pick_rows<MT>(rows, grid);
   if constexpr (MT == 1) {
-    if (small_wg(rows, a.v[0].k)) {
+    if (small_wg(rows, a.v[0].k, NORM ? kXItNorm<F> : kXIt)) {
       /* 256 workgroups of kWavesSmall waves, two or more rows per wave */
       const uint32_t g8 = min(256u, (rows + 2u * kWavesSmall - 1u) / (2u * kWavesSmall));
       const uint32_t rw = (rows + g8 * kWavesSmall - 1u) / (g8 * kWavesSmall);
-      if (rw >= 4u) return launch_u<F, 4, 1, false, kWavesSmall>(a, x, ntok, g8, s);
-      return launch_u<F, 2, 1, false, kWavesSmall>(a, x, ntok, g8, s);
+      if (rw >= 4u) return launch_u<F, 4, 1, false, kWavesSmall, NORM>(a, x, ntok, g8, s);
+      return launch_u<F, 2, 1, false, kWavesSmall, NORM>(a, x, ntok, g8, s);
     }
-    if (u == 4) return launch_u<F, 4, 1, false>(a, x, ntok, grid, s);
-    if (u == 2) return launch_u<F, 2, 1, false>(a, x, ntok, grid, s);
-    return launch_u<F, 1, 1, false>(a, x, ntok, grid, s);
+    if (u == 4) return launch_u<F, 4, 1, false, kWaves, NORM>(a, x, ntok, grid, s);
+    if (u == 2) return launch_u<F, 2, 1, false, kWaves, NORM>(a, x, ntok, grid, s);
+    return launch_u<F, 1, 1, false, kWaves, NORM>(a, x, ntok, grid, s);
   } else if constexpr (MT == 2) {
     if (u == 4) return launch_u<F, 4, 2, false>(a, x, ntok, grid, s);
     if (u == 2) return launch_u<F, 2, 2, false>(a, x, ntok, grid, s);
@@ -498,15 +555,40 @@ static hipError_t launch_gemv(const GemvArgs &a, const float *x, uint32_t ntok, 
 /* Paired gate/up launch: grid sized for both matrices' rows; a row group
  * holds 2 rows of each matrix when waves get 2 or more rows (and MT <= 2),
  * else 1. */
-template <class F, int MT>
+template <class F, int MT, bool NORM = false>
 static hipError_t launch_pair(const GemvArgs &a, const float *x, uint32_t ntok, hipStream_t s) {
   const uint32_t n = a.v[0].n;
   const uint32_t grid = pick_grid(2u * n, 1u);
   const uint32_t rw = (n + grid * kWaves - 1u) / (grid * kWaves);
   if constexpr (MT <= 2) {
-    if (rw >= 2u) return launch_u<F, 4, MT, true>(a, x, ntok, grid, s);
+    if (rw >= 2u) return launch_u<F, 4, MT, true, kWaves, NORM>(a, x, ntok, grid, s);
   }
-  return launch_u<F, 2, MT, true>(a, x, ntok, grid, s);
+  return launch_u<F, 2, MT, true, kWaves, NORM>(a, x, ntok, grid, s);
+}
+
+/* One token through the integer-dot kernel with the decode step's fusions:
+ * gamma set, x is RMSNorm-ed on the way in; accum set, the products are
+ * added to y; pair set, vs = {gate, up} and ys[0] = silu(gate) * up. */
+template <class F>
+static hipError_t gemv_one(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                           int pair, const float *x, const float *gamma, float eps, int accum,
+                           hipStream_t s) {
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.count = count;
+  for (uint32_t i = 0; i < count; ++i) {
+    a.v[i] = *vs[i];
+    a.y[i] = ys[i];
+  }
+  a.accum = accum ? 1u : 0u;
+  a.gamma = gamma;
+  a.eps = eps;
+  if (pair) {
+    if (gamma != nullptr) return launch_pair<F, 1, true>(a, x, 1u, s);
+    return launch_pair<F, 1>(a, x, 1u, s);
+  }
+  if (gamma != nullptr) return launch_gemv<F, 1, true>(a, x, 1u, s);
+  return launch_gemv<F, 1>(a, x, 1u, s);
 }
 
 /* Calls of two or more tokens run on the matrix-core kernel (qgemv_mx.hip)
@@ -575,6 +657,9 @@ static hipError_t gemv_pair_tokens(const paik_qview_t *vg, const paik_qview_t *v
 using namespace paik;
 
 extern "C" uint32_t paik_gemv_pair_max_k(void) { return slice_cap(1u) * 32u; }
+extern "C" uint32_t paik_gemv_norm_max_k(uint32_t type) {
+  return slice_cap(1u, kWaves, type == 8u ? kXItNorm<Q8_0> : kXItNorm<Q4_K>) * 32u;
+}
 
 extern "C" int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up, uint32_t m,
                                   const float *x, float *h, void *stream) {
@@ -599,6 +684,23 @@ extern "C" int paik_gemv_multi(const paik_qview_t *const *vs, float *const *ys, 
   case 2u: return (int)gemv_tokens<Q4_0>(vs, ys, count, m, x, s);
   case 12u: return (int)gemv_tokens<Q4_K>(vs, ys, count, m, x, s);
   case 14u: return (int)gemv_tokens<Q6_K>(vs, ys, count, m, x, s);
+  default: return (int)hipErrorInvalidValue;
+  }
+}
+
+extern "C" int paik_gemv_one(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                             int pair, const float *x, const float *gamma, float eps, int accum,
+                             void *stream) {
+  if (count == 0u || count > (uint32_t)kMaxMats) return (int)hipErrorInvalidValue;
+  if (pair && (count != 2u || accum || vs[0]->n != vs[1]->n)) return (int)hipErrorInvalidValue;
+  for (uint32_t i = 1; i < count; ++i)
+    if (vs[i]->type != vs[0]->type || vs[i]->k != vs[0]->k) return (int)hipErrorInvalidValue;
+  hipStream_t s = (hipStream_t)stream;
+  switch (vs[0]->type) {
+  case 8u: return (int)gemv_one<Q8_0>(vs, ys, count, pair, x, gamma, eps, accum, s);
+  case 2u: return (int)gemv_one<Q4_0>(vs, ys, count, pair, x, gamma, eps, accum, s);
+  case 12u: return (int)gemv_one<Q4_K>(vs, ys, count, pair, x, gamma, eps, accum, s);
+  case 14u: return (int)gemv_one<Q6_K>(vs, ys, count, pair, x, gamma, eps, accum, s);
   default: return (int)hipErrorInvalidValue;
   }
 }

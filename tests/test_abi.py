@@ -151,6 +151,13 @@ def test_decode_entry_points_reject_bad_arguments_before_device():
     assert lib.pai_rope_kv_append_async(*args, 4, 2, 64, 32, 16, 16, None) == -1
     assert lib.pai_rope_kv_append_async(*args, 4, 2, 64, 40, 16, 0, None) == -3
     assert lib.pai_rope_kv_append_async(*args, 4, 2, 512, 32, 16, 0, None) == -3
+    # fused norm / residual projections: NULL arguments and matrix counts
+    assert lib.pai_qgemv_rmsnorm_f32_async(None, 1, fake, fake, 0.0, fake, None) == -1
+    assert lib.pai_qgemv_rmsnorm_f32_async(fake, 0, fake, fake, 0.0, fake, None) == -1
+    assert lib.pai_qgemv_rmsnorm_f32_async(fake, 5, fake, fake, 0.0, fake, None) == -1
+    assert lib.pai_qgemv_rmsnorm_gate_up_async(None, fake, fake, fake, 0.0, fake, None) == -1
+    assert lib.pai_qgemv_add_f32_async(None, fake, fake, None) == -1
+    assert lib.pai_qgemv_add_f32_async(fake, None, fake, None) == -1
     # norm and argmax sizes
     assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 0, 0.0, None) == -1
     assert lib.pai_rmsnorm_f32_async(fake, None, fake, fake, 16385, 0.0, None) == -3

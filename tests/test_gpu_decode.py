@@ -20,6 +20,7 @@ Bars:
                             within 1e-4 of each other (relative to the
                             largest logit)
 """
+import ctypes as C
 import sys
 
 import numpy as np
@@ -79,6 +80,94 @@ def test_rmsnorm(n, with_delta):
     assert np.array_equal(bx.download(n).view(np.uint32), xs.view(np.uint32))
     want = ob.rmsnorm(xs, g)
     assert np.array_equal(bo.download(n).view(np.uint32), want.view(np.uint32))
+
+
+FUSED_CASES = [(pa.Q4_K, 4096, 1024), (pa.Q6_K, 14336, 512), (pa.Q4_0, 256, 300),
+               (pa.Q8_0, 2048, 96)]
+
+
+def packed(qtype, n, k, seed):
+    w = pa.normal_f32(seed, n * k, 0.0, 0.02).reshape(n, k)
+    blocks = pa.quantize(qtype, w)
+    return blocks, pa.QMat(qtype, n, k, blocks)
+
+
+def ptr_array(ptrs):
+    return (C.c_void_p * len(ptrs))(*ptrs)
+
+
+@pytest.mark.parametrize("qtype,k,n", FUSED_CASES)
+def test_fused_rmsnorm_projections(qtype, k, n):
+    """rmsnorm(x) W_i^T in one launch (one, then three matrices) against the
+    oracle's RMSNorm followed by its sequential qgemm, and bit for bit
+    against pai_rmsnorm_f32_async followed by pai_qgemm_f32_multi_async."""
+    say(f"[gpu] fused rmsnorm+gemv type={qtype} k={k} n={n}")
+    rng = np.random.default_rng(k + n)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    mats = [packed(qtype, n + 32 * i, k, 0xF00 + 16 * qtype + i) for i in range(3)]
+    bx, bg, bxn = dev(x), dev(g), hm.DeviceBuffer(4 * k)
+    xn = ob.rmsnorm(x, g)
+    for count in (1, 3):
+        ys = [hm.DeviceBuffer(4 * (n + 32 * i)) for i in range(count)]
+        ys2 = [hm.DeviceBuffer(4 * (n + 32 * i)) for i in range(count)]
+        hs = ptr_array([m.handle for _, m in mats[:count]])
+        check(lib().pai_qgemv_rmsnorm_f32_async(hs, count, bx.ptr, bg.ptr, 0.0,
+                                                ptr_array([y.ptr for y in ys]), None),
+              "pai_qgemv_rmsnorm_f32_async")
+        check(lib().pai_rmsnorm_f32_async(bx.ptr, None, bg.ptr, bxn.ptr, k, 0.0, None),
+              "pai_rmsnorm_f32_async")
+        check(lib().pai_qgemm_f32_multi_async(hs, count, 1, bxn.ptr,
+                                              ptr_array([y.ptr for y in ys2]),
+                                              pa.FLAG_DEVICE_PTRS, None),
+              "pai_qgemm_f32_multi_async")
+        hm.synchronize()
+        for i in range(count):
+            blocks, _ = mats[i]
+            ni = n + 32 * i
+            got = ys[i].download(ni)
+            want = ob.qgemm_seq(qtype, ni, k, blocks, xn.reshape(1, k)).reshape(ni)
+            assert rel_l2(got, want) <= 1e-5, (count, i)
+            assert np.array_equal(got.view(np.uint32), ys2[i].download(ni).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype,k,n", FUSED_CASES)
+def test_fused_rmsnorm_gate_up(qtype, k, n):
+    say(f"[gpu] fused rmsnorm+gate/up type={qtype} k={k} n={n}")
+    rng = np.random.default_rng(3 * k + n)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    (gb, wg), (ub, wu) = packed(qtype, n, k, 0xA11 + qtype), packed(qtype, n, k, 0xB22 + qtype)
+    bx, bg, bh = dev(x), dev(g), hm.DeviceBuffer(4 * n)
+    check(lib().pai_qgemv_rmsnorm_gate_up_async(wg.handle, wu.handle, bx.ptr, bg.ptr, 0.0, bh.ptr,
+                                                None), "pai_qgemv_rmsnorm_gate_up_async")
+    hm.synchronize()
+    xn = ob.rmsnorm(x, g).reshape(1, k)
+    want = ob.silu_mul(ob.qgemm_seq(qtype, n, k, gb, xn), ob.qgemm_seq(qtype, n, k, ub, xn))
+    assert rel_l2(bh.download(n), want.reshape(n)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype,k,n", FUSED_CASES)
+def test_projection_adds_to_residual(qtype, k, n):
+    """y += x W^T: one f32 add of the finished product per output, as the
+    reference's GEMM then ADD; called twice in a row (the decode step adds
+    o and down to the same residual)."""
+    say(f"[gpu] gemv+add type={qtype} k={k} n={n}")
+    rng = np.random.default_rng(5 * k + n)
+    x = rng.standard_normal(k).astype(np.float32)
+    y0 = rng.standard_normal(n).astype(np.float32)
+    blocks, w = packed(qtype, n, k, 0xC33 + qtype)
+    bx, by, bp = dev(x), dev(y0), hm.DeviceBuffer(4 * n)
+    check(lib().pai_qgemv_add_f32_async(w.handle, bx.ptr, by.ptr, None), "pai_qgemv_add_f32_async")
+    w.gemm_async(bx.ptr, bp.ptr, 1)
+    hm.synchronize()
+    prod = bp.download(n)
+    assert rel_l2(prod, ob.qgemm_seq(qtype, n, k, blocks, x.reshape(1, k)).reshape(n)) <= 1e-5
+    y1 = by.download(n)
+    assert np.array_equal(y1.view(np.uint32), (y0 + prod).view(np.uint32))
+    check(lib().pai_qgemv_add_f32_async(w.handle, bx.ptr, by.ptr, None), "pai_qgemv_add_f32_async")
+    hm.synchronize()
+    assert np.array_equal(by.download(n).view(np.uint32), (y1 + prod).view(np.uint32))
 
 
 @pytest.mark.parametrize("hq,hk,hd,r2", [(32, 8, 128, 64), (4, 2, 64, 16), (2, 1, 256, 128)])
