@@ -183,16 +183,24 @@ __device__ __forceinline__ float f16hi(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-/* element i of a RoPE-rotated row (pai_ref_rope_f32's arithmetic) */
-__device__ __forceinline__ float rope_at(const float *__restrict__ src, uint32_t i, uint32_t r2,
-                                         const float *__restrict__ cos_t,
-                                         const float *__restrict__ sin_t) {
-  if (i < r2) return src[i] * cos_t[i] - src[i + r2] * sin_t[i];
-  if (i < 2u * r2) return src[i - r2] * sin_t[i - r2] + src[i] * cos_t[i - r2];
-  return src[i];
+/* RoPE's pairing for element i of a head (pai_ref_rope_f32's
+ * arithmetic): i < r2 pairs with i + r2 and uses table entry i; r2 <= i <
+ * 2 r2 pairs with i - r2 and uses entry i - r2; the rest are not rotated
+ * (partner i, entry 0, unused). */
+__device__ __forceinline__ void rope_pair(uint32_t i, uint32_t r2, uint32_t &partner,
+                                          uint32_t &entry) {
+  partner = i < r2 ? i + r2 : (i < 2u * r2 ? i - r2 : i);
+  entry = i < r2 ? i : (i < 2u * r2 ? i - r2 : 0u);
+}
+/* the rotated value from x[i], x[partner], cos and sin of the entry */
+__device__ __forceinline__ float rope_val(uint32_t i, uint32_t r2, float xi, float xp, float c,
+                                          float s) {
+  if (i < r2) return xi * c - xp * s;
+  if (i < 2u * r2) return xp * s + xi * c;
+  return xi;
 }
 
-template <int HD>
+template <int HD, bool ROPE>
 __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
                                               const float *__restrict__ knew,
                                               const float *__restrict__ vnew,
@@ -204,6 +212,7 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
   constexpr int LP = HD / 8;   /* lanes per row */
   constexpr int PPI = 64 / LP; /* rows per wave instruction */
   constexpr int IT = 16 / PPI; /* iterations over a wave's 16 rows */
+  constexpr int QPT = kMaxG * HD / 256; /* q elements per thread, at most */
   __shared__ float qs[kMaxG][HD];
   __shared__ float nk[HD], nv[HD];
   __shared__ float sm[4][kMaxG], sl[4][kMaxG];
@@ -215,10 +224,41 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
   _Float16 *kb = kc + (size_t)kvh * ctx * HD;
   _Float16 *vb = vc + (size_t)kvh * ctx * HD;
   const uint32_t base = c * kChunk + wave * 16u;
-  const bool append = knew != nullptr;
   const uint32_t pos = len - 1u;
 
-  /* this lane's rows: 8 K and 8 V values each, loads issued first */
+  /* The small loads go first, unconditionally (indices clamped into
+   * range), so they return ahead of the K/V stream and nothing waits on a
+   * branch: q of the G heads of this KV head (consecutive in q), with
+   * RoPE's partner element and table entries, and the step's new k, v. */
+  const float *qg = q + (size_t)kvh * G * HD;
+  const uint32_t nq = G * (uint32_t)HD;
+  float qa[QPT], qb[QPT], qc[QPT], qn[QPT];
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+    const uint32_t e = min(threadIdx.x + 256u * (uint32_t)j, nq - 1u);
+    const uint32_t i = e % (uint32_t)HD;
+    qa[j] = qg[e];
+    if constexpr (ROPE) {
+      uint32_t pt, en;
+      rope_pair(i, r2, pt, en);
+      qb[j] = qg[e - i + pt];
+      qc[j] = cos_t[en];
+      qn[j] = sin_t[en];
+    }
+  }
+  const uint32_t ni = min(threadIdx.x, (uint32_t)HD - 1u);
+  float ka = 0.f, kp = 0.f, kcs = 0.f, ksn = 0.f, va = 0.f;
+  if constexpr (ROPE) {
+    uint32_t pt, en;
+    rope_pair(ni, r2, pt, en);
+    ka = knew[(size_t)kvh * HD + ni];
+    kp = knew[(size_t)kvh * HD + pt];
+    va = vnew[(size_t)kvh * HD + ni];
+    kcs = cos_t[en];
+    ksn = sin_t[en];
+  }
+
+  /* this lane's rows: 8 K and 8 V values each */
   uint4 kw[IT], vw[IT];
   bool ok[IT];
 #pragma unroll
@@ -229,20 +269,27 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
     kw[it] = *reinterpret_cast<const uint4 *>(kb + (size_t)pc * HD + 8u * t);
     vw[it] = *reinterpret_cast<const uint4 *>(vb + (size_t)pc * HD + 8u * t);
   }
-  /* q of the G heads (rotated when appending) */
-  for (uint32_t e = threadIdx.x; e < G * (uint32_t)HD; e += blockDim.x) {
-    const uint32_t g = e / HD, i = e % HD;
-    const float *src = q + (size_t)(kvh * G + g) * HD;
-    qs[g][i] = append ? rope_at(src, i, r2, cos_t, sin_t) : src[i];
+  /* q of the G heads (rotated for the append form) into LDS; threads past
+   * the end repeat the last element with its own value (no branch, so the
+   * loads above stay ahead of the K/V stream) */
+#pragma unroll
+  for (int j = 0; j < QPT; ++j) {
+    const uint32_t e = min(threadIdx.x + 256u * (uint32_t)j, nq - 1u);
+    const uint32_t i = e % (uint32_t)HD;
+    (&qs[0][0])[e] = ROPE ? rope_val(i, r2, qa[j], qb[j], qc[j], qn[j]) : qa[j];
   }
-  if (append && pos / kChunk == c) {
-    for (uint32_t i = threadIdx.x; i < (uint32_t)HD; i += blockDim.x) {
-      const _Float16 kh = (_Float16)rope_at(knew + (size_t)kvh * HD, i, r2, cos_t, sin_t);
-      const _Float16 vh = (_Float16)vnew[(size_t)kvh * HD + i];
-      kb[(size_t)pos * HD + i] = kh;
-      vb[(size_t)pos * HD + i] = vh;
-      nk[i] = (float)kh;
-      nv[i] = (float)vh;
+  /* The new k (rotated) and v in fp16: every workgroup forms them into
+   * LDS (threads past HD repeat element HD - 1 with the same value), so
+   * their loads stay ahead of the K/V stream; the chunk holding position
+   * pos also stores them in the cache and uses these copies. */
+  if constexpr (ROPE) {
+    const _Float16 kh = (_Float16)rope_val(ni, r2, ka, kp, kcs, ksn);
+    const _Float16 vh = (_Float16)va;
+    nk[ni] = (float)kh;
+    nv[ni] = (float)vh;
+    if (pos / kChunk == c && threadIdx.x < (uint32_t)HD) {
+      kb[(size_t)pos * HD + ni] = kh;
+      vb[(size_t)pos * HD + ni] = vh;
     }
   }
   __syncthreads();
@@ -259,7 +306,7 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
       vr[it][2 * e] = f16lo(va[e]);
       vr[it][2 * e + 1] = f16hi(va[e]);
     }
-    if (append && base + (uint32_t)(it * PPI) + slot == pos) { /* this step's row */
+    if (ROPE && base + (uint32_t)(it * PPI) + slot == pos) { /* this step's row */
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         kr[it][e] = nk[8u * t + e];
@@ -346,20 +393,20 @@ __global__ void __launch_bounds__(HD) k_attn_merge(const float *__restrict__ par
   const size_t cstep = (size_t)G * stride; /* floats from one chunk's triple to the next */
   const float *pk = part + ((size_t)kvh * nch * G + g) * stride;
   if (threadIdx.x < 64u) {
+    /* (m, l) of every chunk: clamped, unconditional loads, masked after */
     const uint32_t lane = threadIdx.x;
     float mv[PER], lv[PER];
     float M = -INFINITY;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const uint32_t cc = lane + 64u * (uint32_t)j;
-      mv[j] = -INFINITY;
-      lv[j] = 0.0f;
-      if (cc < nch) {
-        mv[j] = pk[cc * cstep];
-        lv[j] = pk[cc * cstep + 1u];
-      }
-      M = fmaxf(M, mv[j]);
+      const size_t at = (size_t)min(cc, nch - 1u) * cstep;
+      mv[j] = pk[at];
+      lv[j] = pk[at + 1u];
     }
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (lane + 64u * (uint32_t)j < nch) M = fmaxf(M, mv[j]);
     for (int sh = 32; sh > 0; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
     float L = 0.0f;
 #pragma unroll
@@ -375,11 +422,18 @@ __global__ void __launch_bounds__(HD) k_attn_merge(const float *__restrict__ par
     if (lane == 0u) sL = L;
   }
   __syncthreads();
+  /* o: the chunks' partial sums in chunk order, loaded 32 at a time */
   const uint32_t d = threadIdx.x;
   const float *pc = pk + 2u + d;
   float acc = 0.0f;
-#pragma unroll 8
-  for (uint32_t cc = 0; cc < nch; ++cc) acc = fmaf(pc[cc * cstep], fsc[cc], acc);
+  for (uint32_t c0 = 0; c0 < nch; c0 += 32u) {
+    float ov[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) ov[j] = pc[(size_t)min(c0 + (uint32_t)j, nch - 1u) * cstep];
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      if (c0 + (uint32_t)j < nch) acc = fmaf(ov[j], fsc[c0 + (uint32_t)j], acc);
+  }
   o[(size_t)h * HD + d] = acc / sL;
 }
 
@@ -511,25 +565,24 @@ extern "C" int paik_attn_decode(const float *q, const float *knew, const float *
   const uint32_t G = hq / hk, nch = paik_attn_chunks(len);
   hipStream_t s = (hipStream_t)stream;
   _Float16 *k16 = static_cast<_Float16 *>(kc), *v16 = static_cast<_Float16 *>(vc);
+  const bool rope = knew != nullptr;
+#define PAIK_ATTN(HD)                                                                            \
+  do {                                                                                           \
+    if (rope)                                                                                    \
+      k_attn<HD, true><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, \
+                                                G, ctx, len, nch);                               \
+    else                                                                                         \
+      k_attn<HD, false><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16,      \
+                                                 part, G, ctx, len, nch);                        \
+    k_attn_merge<HD><<<hq, HD, 0, s>>>(part, o, G, nch);                                         \
+  } while (0)
   switch (hd) {
-  case 64:
-    k_attn<64><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
-                                        len, nch);
-    k_attn_merge<64><<<hq, 64, 0, s>>>(part, o, G, nch);
-    break;
-  case 128:
-    k_attn<128><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
-                                         len, nch);
-    k_attn_merge<128><<<hq, 128, 0, s>>>(part, o, G, nch);
-    break;
-  case 256:
-    k_attn<256><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, G, ctx,
-                                         len, nch);
-    k_attn_merge<256><<<hq, 256, 0, s>>>(part, o, G, nch);
-    break;
-  default:
-    return (int)hipErrorInvalidValue;
+  case 64: PAIK_ATTN(64); break;
+  case 128: PAIK_ATTN(128); break;
+  case 256: PAIK_ATTN(256); break;
+  default: return (int)hipErrorInvalidValue;
   }
+#undef PAIK_ATTN
   return (int)hipGetLastError();
 }
 
