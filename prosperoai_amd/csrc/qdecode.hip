@@ -176,6 +176,32 @@ constexpr uint32_t kChunk = 64;
 constexpr uint32_t kMaxG = 8;
 constexpr uint32_t kMaxChunks = 512; /* len <= 32768 */
 
+/* Reductions over aligned groups of L lanes (L <= 16) on DPP: quad swaps,
+ * then the 8-lane half-row and 16-lane row mirrors (sum and max are
+ * symmetric, so mirrored partners combine like butterflies). */
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int L>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(L <= 16, "DPP covers one 16-lane row");
+  if constexpr (L >= 2) v += dpp_f<0xB1>(v);  /* quad: lane ^ 1 */
+  if constexpr (L >= 4) v += dpp_f<0x4E>(v);  /* quad: lane ^ 2 */
+  if constexpr (L >= 8) v += dpp_f<0x141>(v); /* row_half_mirror */
+  if constexpr (L >= 16) v += dpp_f<0x140>(v); /* row_mirror */
+  return v;
+}
+/* Sum over groups of L lanes: DPP within a row, shuffles across rows. */
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  v = row_sum<(L < 16 ? L : 16)>(v);
+  if constexpr (L >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 __device__ __forceinline__ float f16lo(uint32_t w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
 }
@@ -200,7 +226,7 @@ __device__ __forceinline__ float rope_val(uint32_t i, uint32_t r2, float xi, flo
   return xi;
 }
 
-template <int HD, bool ROPE>
+template <int HD, bool ROPE, int GM>
 __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
                                               const float *__restrict__ knew,
                                               const float *__restrict__ vnew,
@@ -212,11 +238,12 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
   constexpr int LP = HD / 8;   /* lanes per row */
   constexpr int PPI = 64 / LP; /* rows per wave instruction */
   constexpr int IT = 16 / PPI; /* iterations over a wave's 16 rows */
-  constexpr int QPT = kMaxG * HD / 256; /* q elements per thread, at most */
-  __shared__ float qs[kMaxG][HD];
+  constexpr int QPT = (GM * HD + 255) / 256; /* q elements per thread, at most */
+  static_assert(GM >= 1 && GM <= (int)kMaxG, "head group");
+  __shared__ float qs[GM][HD];
   __shared__ float nk[HD], nv[HD];
-  __shared__ float sm[4][kMaxG], sl[4][kMaxG];
-  __shared__ float so[4][kMaxG][HD];
+  __shared__ float sm[4][GM], sl[4][GM];
+  __shared__ float so[4][GM][HD];
   const uint32_t kvh = blockIdx.x / nch, c = blockIdx.x % nch;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t slot = lane / LP, t = lane % LP;
@@ -315,44 +342,68 @@ __global__ void __launch_bounds__(256) k_attn(const float *__restrict__ q,
     }
   }
 
-  for (uint32_t g = 0; g < G; ++g) {
+  /* Scores, softmax terms and weighted v of the GM head slots (heads g <
+   * G are real): unrolled over the heads, so their reduction chains
+   * overlap. A row's dot product is summed over its LP lanes on DPP; the
+   * wave's PPI rows combine across rows with shuffles. */
+  float s[GM][IT];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
     float qv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) qv[e] = qs[g][8u * t + e];
-    float s[IT];
-    float m = -INFINITY;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       float d = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) d = fmaf(qv[e], kr[it][e], d);
-#pragma unroll
-      for (int sh = LP / 2; sh > 0; sh >>= 1) d += __shfl_xor(d, sh, 64);
-      s[it] = ok[it] ? d * scale : -INFINITY;
-      m = fmaxf(m, s[it]);
+      d = lane_group_sum<LP>(d);
+      s[g][it] = ok[it] ? d * scale : -INFINITY;
     }
+  }
+  float m[GM];
 #pragma unroll
-    for (int sh = 32; sh >= LP; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh, 64));
-    float l = 0.0f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int g = 0; g < GM; ++g) {
+    m[g] = -INFINITY;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) m[g] = fmaxf(m[g], s[g][it]);
+  }
+#pragma unroll
+  for (int sh = 32; sh >= LP; sh >>= 1)
+#pragma unroll
+    for (int g = 0; g < GM; ++g) m[g] = fmaxf(m[g], __shfl_xor(m[g], sh, 64));
+  float l[GM], acc[GM][8];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    l[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const float e = ok[it] ? expf(s[it] - m) : 0.0f;
-      l += e;
+      const float e = ok[it] ? expf(s[g][it] - m[g]) : 0.0f;
+      l[g] += e;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = fmaf(e, vr[it][j], acc[j]);
+      for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(e, vr[it][j], acc[g][j]);
     }
+  }
 #pragma unroll
-    for (int sh = 32; sh >= LP; sh >>= 1) {
-      l += __shfl_xor(l, sh, 64);
+  for (int sh = 32; sh >= LP; sh >>= 1)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += __shfl_xor(acc[j], sh, 64);
+    for (int g = 0; g < GM; ++g) {
+      l[g] += __shfl_xor(l[g], sh, 64);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] += __shfl_xor(acc[g][j], sh, 64);
     }
-    if (slot == 0u) {
+  if (slot == 0u) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) so[wave][g][8u * t + j] = acc[j];
-      if (t == 0u) {
-        sm[wave][g] = m;
-        sl[wave][g] = l;
+    for (int g = 0; g < GM; ++g) {
+      if ((uint32_t)g < G) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) so[wave][g][8u * t + j] = acc[g][j];
+        if (t == 0u) {
+          sm[wave][g] = m[g];
+          sl[wave][g] = l[g];
+        }
       }
     }
   }
@@ -392,6 +443,14 @@ __global__ void __launch_bounds__(HD) k_attn_merge(const float *__restrict__ par
   const uint32_t h = blockIdx.x, kvh = h / G, g = h % G;
   const size_t cstep = (size_t)G * stride; /* floats from one chunk's triple to the next */
   const float *pk = part + ((size_t)kvh * nch * G + g) * stride;
+  /* The first 64 chunks' partial sums for this thread's element are
+   * requested before the (m, l) loads, so both return in one round trip. */
+  const uint32_t d = threadIdx.x;
+  const float *pc = pk + 2u + d;
+  constexpr int kPre = 64;
+  float ov[kPre];
+#pragma unroll
+  for (int j = 0; j < kPre; ++j) ov[j] = pc[(size_t)min((uint32_t)j, nch - 1u) * cstep];
   if (threadIdx.x < 64u) {
     /* (m, l) of every chunk: clamped, unconditional loads, masked after */
     const uint32_t lane = threadIdx.x;
@@ -422,17 +481,18 @@ __global__ void __launch_bounds__(HD) k_attn_merge(const float *__restrict__ par
     if (lane == 0u) sL = L;
   }
   __syncthreads();
-  /* o: the chunks' partial sums in chunk order, loaded 32 at a time */
-  const uint32_t d = threadIdx.x;
-  const float *pc = pk + 2u + d;
+  /* o: the chunks' partial sums in chunk order */
   float acc = 0.0f;
-  for (uint32_t c0 = 0; c0 < nch; c0 += 32u) {
-    float ov[32];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) ov[j] = pc[(size_t)min(c0 + (uint32_t)j, nch - 1u) * cstep];
+  for (int j = 0; j < kPre; ++j)
+    if ((uint32_t)j < nch) acc = fmaf(ov[j], fsc[j], acc);
+  for (uint32_t c0 = kPre; c0 < nch; c0 += 32u) {
+    float ow[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) ow[j] = pc[(size_t)min(c0 + (uint32_t)j, nch - 1u) * cstep];
 #pragma unroll
     for (int j = 0; j < 32; ++j)
-      if (c0 + (uint32_t)j < nch) acc = fmaf(ov[j], fsc[c0 + (uint32_t)j], acc);
+      if (c0 + (uint32_t)j < nch) acc = fmaf(ow[j], fsc[c0 + (uint32_t)j], acc);
   }
   o[(size_t)h * HD + d] = acc / sL;
 }
@@ -566,15 +626,24 @@ extern "C" int paik_attn_decode(const float *q, const float *knew, const float *
   hipStream_t s = (hipStream_t)stream;
   _Float16 *k16 = static_cast<_Float16 *>(kc), *v16 = static_cast<_Float16 *>(vc);
   const bool rope = knew != nullptr;
-#define PAIK_ATTN(HD)                                                                            \
-  do {                                                                                           \
-    if (rope)                                                                                    \
-      k_attn<HD, true><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, part, \
-                                                G, ctx, len, nch);                               \
-    else                                                                                         \
-      k_attn<HD, false><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16,      \
-                                                 part, G, ctx, len, nch);                        \
-    k_attn_merge<HD><<<hq, HD, 0, s>>>(part, o, G, nch);                                         \
+  /* head-group width: G itself for 1, 2, 4 or 8, else the next of those */
+  const uint32_t gm = G <= 1u ? 1u : G <= 2u ? 2u : G <= 4u ? 4u : 8u;
+#define PAIK_ATTN_G(HD, GMV)                                                                   \
+  do {                                                                                         \
+    if (rope)                                                                                  \
+      k_attn<HD, true, GMV><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16, v16, \
+                                                     part, G, ctx, len, nch);                  \
+    else                                                                                       \
+      k_attn<HD, false, GMV><<<hk * nch, 256, 0, s>>>(q, knew, vnew, cos_t, sin_t, r2, k16,     \
+                                                      v16, part, G, ctx, len, nch);            \
+  } while (0)
+#define PAIK_ATTN(HD)                                                                          \
+  do {                                                                                         \
+    if (gm == 1u) PAIK_ATTN_G(HD, 1);                                                          \
+    else if (gm == 2u) PAIK_ATTN_G(HD, 2);                                                     \
+    else if (gm == 4u) PAIK_ATTN_G(HD, 4);                                                     \
+    else PAIK_ATTN_G(HD, 8);                                                                   \
+    k_attn_merge<HD><<<hq, HD, 0, s>>>(part, o, G, nch);                                       \
   } while (0)
   switch (hd) {
   case 64: PAIK_ATTN(64); break;
@@ -583,6 +652,7 @@ extern "C" int paik_attn_decode(const float *q, const float *knew, const float *
   default: return (int)hipErrorInvalidValue;
   }
 #undef PAIK_ATTN
+#undef PAIK_ATTN_G
   return (int)hipGetLastError();
 }
 
