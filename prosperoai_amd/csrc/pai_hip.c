@@ -30,6 +30,10 @@ struct pai_qmat {
    * guarded by g_x16_lock */
   void *x16;
   uint64_t x16_bytes;
+  /* the up product of a split-K gate/up call (see ywork_workspace); same
+   * lock */
+  void *yw;
+  uint64_t yw_bytes;
 };
 
 /* ---------------------------------------------------------------------- */
@@ -316,6 +320,7 @@ __attribute__((visibility("hidden"))) pai_status_t pai__ready(void) { return ens
 pai_status_t pai_qmat_free(pai_qmat_t *w) {
   if (w == NULL) return PAI_OK;
   if (w->x16 != NULL) (void)hipFree(w->x16);
+  if (w->yw != NULL) (void)hipFree(w->yw);
   hipError_t e = hipFree(w->dev);
   free(w);
   return e == hipSuccess ? PAI_OK : map_hip(e, "hipFree(weights)");
@@ -368,33 +373,52 @@ static int gemv_call(const pai_qmat_t *w, uint64_t m, uint32_t flags) {
 #define PAI_X16_TOKENS 1024u
 static pthread_mutex_t g_x16_lock = PTHREAD_MUTEX_INITIALIZER;
 
-static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint64_t *bytes) {
-  pai_qmat_t *w = (pai_qmat_t *)cw;
-  const uint64_t tok = ((m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS) + 255u) & ~(uint64_t)255u;
-  const uint64_t want = tok * w->k * 2u;
-  pthread_mutex_lock(&g_x16_lock);
-  if (w->x16 == NULL || w->x16_bytes < want) {
+/* A handle-owned device buffer of at least `want` bytes, grown outside
+ * stream capture only (NULL with *bytes = 0, or the smaller buffer, during
+ * capture). Caller holds g_x16_lock. */
+static void *grow_workspace(void **slot, uint64_t *slot_bytes, uint64_t want, hipStream_t s,
+                            uint64_t *bytes) {
+  if (*slot == NULL || *slot_bytes < want) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
       void *p = NULL;
-      if (w->x16 != NULL) {
+      if (*slot != NULL) {
         (void)hipStreamSynchronize(s); /* earlier calls on s may still read it */
-        (void)hipFree(w->x16);
-        w->x16 = NULL;
-        w->x16_bytes = 0;
+        (void)hipFree(*slot);
+        *slot = NULL;
+        *slot_bytes = 0;
       }
       if (hipMalloc(&p, want) == hipSuccess) {
-        w->x16 = p;
-        w->x16_bytes = want;
+        *slot = p;
+        *slot_bytes = want;
       } else {
-        (void)hipGetLastError(); /* no workspace: the register-staged kernels run */
+        (void)hipGetLastError(); /* no workspace: the caller takes its other path */
       }
     }
   }
-  void *p = w->x16;
-  *bytes = w->x16_bytes;
+  *bytes = *slot_bytes;
+  return *slot;
+}
+
+static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint64_t *bytes) {
+  pai_qmat_t *w = (pai_qmat_t *)cw;
+  const uint64_t tok = ((m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS) + 255u) & ~(uint64_t)255u;
+  pthread_mutex_lock(&g_x16_lock);
+  void *p = grow_workspace(&w->x16, &w->x16_bytes, tok * w->k * 2u, s, bytes);
   pthread_mutex_unlock(&g_x16_lock);
   return p;
+}
+
+/* m x n floats for the up product of a split-K gate/up call, owned by the
+ * up matrix's handle; NULL when it cannot be had (inside a capture). */
+static float *ywork_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s) {
+  pai_qmat_t *w = (pai_qmat_t *)cw;
+  const uint64_t want = m * w->n * 4u;
+  uint64_t have = 0;
+  pthread_mutex_lock(&g_x16_lock);
+  void *p = grow_workspace(&w->yw, &w->yw_bytes, want, s, &have);
+  pthread_mutex_unlock(&g_x16_lock);
+  return have >= want ? (float *)p : NULL;
 }
 
 static pai_status_t launch_mfma(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
@@ -403,6 +427,20 @@ static pai_status_t launch_mfma(const pai_qmat_t *w, uint64_t m, const float *x,
   void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(w, m, s, &wb);
   const int e = paik_gemm_mfma(&w->view, (uint32_t)m, x, y, gate,
                                (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, s);
+  return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+}
+
+/* Matrices sharing x in one MFMA launch (the 16-bit path; the
+ * register-staged fallback launches them one by one). */
+static pai_status_t launch_mfma_multi(const pai_qmat_t *const *ws, uint32_t count, uint64_t m,
+                                      const float *x, float *const *ys, uint32_t flags,
+                                      hipStream_t s) {
+  uint64_t wb = 0;
+  void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(ws[0], m, s, &wb);
+  const paik_qview_t *vs[4];
+  for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
+  const int e = paik_gemm_mfma_multi(vs, ys, count, (uint32_t)m, x, NULL,
+                                     (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, s);
   return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
 }
 
@@ -454,11 +492,7 @@ pai_status_t pai_qgemm_f32_multi_async(const pai_qmat_t *const *ws, uint32_t cou
     const int e = paik_gemv_multi(vs, ys, count, (uint32_t)m, x, s);
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
-  for (uint32_t i = 0; i < count; ++i) {
-    pai_status_t st = launch(ws[i], m, x, ys[i], flags, s);
-    if (st != PAI_OK) return st;
-  }
-  return PAI_OK;
+  return launch_mfma_multi(ws, count, m, x, ys, flags, s);
 }
 
 pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qmat_t *w_up,
@@ -483,10 +517,22 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
     const int e = paik_gemv_silu_mul(&w_gate->view, &w_up->view, (uint32_t)m, x, h, s);
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
-  /* the gate product lands in h; the up product's epilogue turns each
-   * element into silu(gate) * up in place */
+  /* The gate product lands in h. When the up product splits over K (few
+   * tiles: batched decode), it lands in a workspace and a third launch
+   * forms silu(gate) * up; otherwise the up product's epilogue does that
+   * in place (whole sums, no split). */
   st = launch_mfma(w_gate, m, x, h, NULL, flags, s);
   if (st != PAI_OK) return st;
+  if (paik_gemm_x16_splits(&w_up->view, (uint32_t)(m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS)) > 1u &&
+      getenv("PAI_GEMM_NO_X16") == NULL) {
+    float *u = ywork_workspace(w_up, m, s);
+    if (u != NULL) {
+      st = launch_mfma(w_up, m, x, u, NULL, flags, s);
+      if (st != PAI_OK) return st;
+      const int e = paik_silu_mul_inplace(h, u, m * w_up->n, s);
+      return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+    }
+  }
   return launch_mfma(w_up, m, x, h, h, flags, s);
 }
 

@@ -122,6 +122,15 @@ int paik_dequant_row(const paik_qview_t *v, const uint32_t *row, float *out,
 int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
                    float *y, const float *gate, int bf16, void *x16,
                    uint64_t x16_bytes, void *stream);
+/* The same for count (1..4) matrices of one format and K sharing x, in one
+ * launch on the 16-bit path (y_i = x W_i^T; gate only with count 1). */
+int paik_gemm_mfma_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                         uint32_t m, const float *x, const float *gate, int bf16, void *x16,
+                         uint64_t x16_bytes, void *stream);
+/* K parts a 16-bit-path launch of m tokens (no gate) splits into. */
+uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m);
+/* h = silu(h) * u over n floats. */
+int paik_silu_mul_inplace(float *h, const float *u, uint64_t n, void *stream);
 
 #ifdef __cplusplus
 }

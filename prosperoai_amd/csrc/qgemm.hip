@@ -240,6 +240,7 @@ struct GLoad<Q6_K> {
   }
 };
 
+constexpr int kGemmMats = 4; /* matrices of one multi-matrix launch */
 struct GemmArgs {
   paik_qview_t v;
   const float *x;
@@ -254,6 +255,12 @@ struct GemmArgs {
   uint32_t per_xcd;                  /* workgroups per XCD */
   uint32_t x_bytes;                  /* m * k * 4 (< 2^31) */
   uint32_t steps_per_split;
+  /* k_gemm_x16 multi-matrix launches: matrices 0..count-1 (same format and
+   * K, matrix 0 being v / y) own row tiles [tile_end[i-1], tile_end[i]) */
+  uint32_t count;
+  uint32_t tile_end[kGemmMats];
+  paik_qview_t mv[kGemmMats];
+  float *my[kGemmMats];
 };
 
 /* Tile shapes: TT tokens x RWG weight rows, NW waves of RWG/NW rows; XB
@@ -517,13 +524,23 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
   static_assert(RF >= 1 && XQ >= 1 && NT <= 512, "tile shape");
   __shared__ __attribute__((aligned(16))) uint8_t Xb[kLdsBytes];
 
-  const paik_qview_t &v = a.v;
   const uint32_t logical = (blockIdx.x % kXcds) * a.per_xcd + blockIdx.x / kXcds;
   const uint32_t ntile = a.tiles_n * a.tiles_m;
   if (logical >= ntile * a.splits) return;
   const uint32_t split = logical / ntile, tile = logical % ntile;
   const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
-  const uint32_t n0 = tn * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
+  /* the matrix owning row tile tn (workgroup-uniform) */
+  paik_qview_t v = a.v;
+  float *ybase = a.y;
+  uint32_t tl = tn;
+#pragma unroll
+  for (int i = 1; i < kGemmMats; ++i)
+    if ((uint32_t)i < a.count && tn >= a.tile_end[i - 1]) {
+      v = a.mv[i];
+      ybase = a.my[i];
+      tl = tn - a.tile_end[i - 1];
+    }
+  const uint32_t n0 = tl * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
   const uint32_t s0 = split * a.steps_per_split;
   const uint32_t s1 = s0 + a.steps_per_split;
@@ -696,9 +713,9 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
-        if (split_k) unsafeAtomicAdd(a.y + at, val);
-        else if (a.gate != nullptr) a.y[at] = silu_mul(a.gate[at], val);
-        else a.y[at] = val;
+        if (split_k) unsafeAtomicAdd(ybase + at, val);
+        else if (a.gate != nullptr) ybase[at] = silu_mul(a.gate[at], val);
+        else ybase[at] = val;
       }
     }
   }
@@ -733,7 +750,7 @@ static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
  * would leave most of the 256 CUs idle (at least 8 steps per split), the
  * step count per split a multiple of 4. */
 static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
-  a.tiles_n = (a.v.n + rwg - 1u) / rwg;
+  if (a.count <= 1u) a.tiles_n = (a.v.n + rwg - 1u) / rwg; /* else set by the caller */
   a.tiles_m = (a.m + tt - 1u) / tt;
   const uint32_t tiles = a.tiles_n * a.tiles_m;
   const uint32_t nsteps = ((a.v.k >> 5) + 3u) >> 2;
@@ -773,8 +790,10 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
 }
 
 template <class F, int TT, int NW, int RWG>
-static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, uint16_t *x16,
-                             float *y, const float *gate, bool bf16, hipStream_t s) {
+static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                             uint32_t m, const float *x, uint16_t *x16, const float *gate,
+                             bool bf16, hipStream_t s) {
+  const paik_qview_t &v = *vs[0];
   const size_t n4 = (size_t)m * v.k / 4u;
   const size_t blocks = (n4 + 255u) / 256u;
   k_cvt_x<><<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
@@ -785,14 +804,25 @@ static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, 
   memset(&a, 0, sizeof a);
   a.v = v;
   a.x16 = x16;
-  a.y = y;
+  a.y = ys[0];
   a.gate = gate;
   a.m = m;
+  a.count = count;
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    a.mv[i] = *vs[i];
+    a.my[i] = ys[i];
+    tiles += (vs[i]->n + (uint32_t)RWG - 1u) / (uint32_t)RWG;
+    a.tile_end[i] = tiles;
+  }
+  a.tiles_n = tiles;
   plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 2u);
   if (a.splits > 1u) {
-    e = zero_fill(y, (size_t)m * v.n, s);
-    if (e != hipSuccess) return e;
+    for (uint32_t i = 0; i < count; ++i) {
+      e = zero_fill(ys[i], (size_t)m * vs[i]->n, s);
+      if (e != hipSuccess) return e;
+    }
   }
   const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
   if (bf16) k_gemm_x16<F, true, TT, NW, RWG><<<grid, block, 0, s>>>(a);
@@ -801,9 +831,10 @@ static hipError_t launch_x16(const paik_qview_t &v, uint32_t m, const float *x, 
 }
 
 template <class F>
-static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x, float *y,
-                              const float *gate, bool bf16, uint16_t *x16, size_t x16_bytes,
-                              hipStream_t s) {
+static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                              uint32_t m, const float *x, const float *gate, bool bf16,
+                              uint16_t *x16, size_t x16_bytes, hipStream_t s) {
+  const paik_qview_t &v = *vs[0];
   /* token blocks whose activations span less than 2^31 bytes (32-bit
    * buffer offsets) and, on the 16-bit path, fit the workspace */
   const size_t row_bytes = (size_t)v.k * 4u;
@@ -817,24 +848,36 @@ static hipError_t launch_gemm(const paik_qview_t &v, uint32_t m, const float *x,
   for (uint32_t t0 = 0; t0 < m; t0 += blk) {
     const uint32_t mt = m - t0 < blk ? m - t0 : blk;
     const float *xt = x + (size_t)t0 * v.k;
-    float *yt = y + (size_t)t0 * v.n;
+    float *yt[kGemmMats];
+    for (uint32_t i = 0; i < count; ++i) yt[i] = ys[i] + (size_t)t0 * vs[i]->n;
     const float *gt = gate != nullptr ? gate + (size_t)t0 * v.n : nullptr;
     /* up to 32 tokens: 32-token tiles; up to 255: 128 x 256 tiles on 8
      * waves; from 256 tokens: 256 x 128 tiles on 4 waves (each weight
-     * value dequantized once per 256 tokens) */
-    hipError_t e;
+     * value dequantized once per 256 tokens). The 16-bit path takes all
+     * matrices in one launch; the register-staged path one per matrix. */
+    hipError_t e = hipSuccess;
     if (use16) {
-      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(v, mt, xt, x16, yt, gt, bf16, s)
-          : mt < 256u ? launch_x16<F, 128, 8, 256>(v, mt, xt, x16, yt, gt, bf16, s)
-                      : launch_x16<F, 256, 4, 128>(v, mt, xt, x16, yt, gt, bf16, s);
+      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, s)
+          : mt < 256u ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, s)
+                      : launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, s);
     } else {
-      e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(v, mt, xt, yt, gt, bf16, s)
-          : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(v, mt, xt, yt, gt, bf16, s)
-                      : launch_tt<F, 256, 4, 128, 1>(v, mt, xt, yt, gt, bf16, s);
+      for (uint32_t i = 0; i < count && e == hipSuccess; ++i)
+        e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, s)
+            : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, s)
+                        : launch_tt<F, 256, 4, 128, 1>(*vs[i], mt, xt, yt[i], gt, bf16, s);
     }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+/* h = silu(h) * u elementwise (the gate/up epilogue as its own launch,
+ * when both products were split over K). */
+template <int = 0>
+__global__ void __launch_bounds__(256) k_silu_mul(float *__restrict__ h,
+                                                  const float *__restrict__ u, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (size_t)gridDim.x * 256u)
+    h[i] = silu_mul(h[i], u[i]);
 }
 
 } // namespace paik
@@ -845,25 +888,51 @@ using namespace paik;
  * Q6_K, entry point PAI_GEMM_ENTRY), so the four formats' GEMM kernels
  * compile in parallel; the unit without PAI_GEMM_FMT holds the dispatcher. */
 #define PAI_GEMM_ARGS                                                                         \
-  const paik_qview_t *v, uint32_t m, const float *x, float *y, const float *gate, int bf16,  \
-      void *x16, uint64_t x16_bytes, void *stream
+  const paik_qview_t *const *vs, float *const *ys, uint32_t count, uint32_t m, const float *x, \
+      const float *gate, int bf16, void *x16, uint64_t x16_bytes, void *stream
 #ifdef PAI_GEMM_FMT
 extern "C" int PAI_GEMM_ENTRY(PAI_GEMM_ARGS) {
-  return (int)launch_gemm<PAI_GEMM_FMT>(*v, m, x, y, gate, bf16 != 0, static_cast<uint16_t *>(x16),
-                                        (size_t)x16_bytes, (hipStream_t)stream);
+  return (int)launch_gemm<PAI_GEMM_FMT>(vs, ys, count, m, x, gate, bf16 != 0,
+                                        static_cast<uint16_t *>(x16), (size_t)x16_bytes,
+                                        (hipStream_t)stream);
 }
 #else
 extern "C" int paik_gemm_mfma_q4_0(PAI_GEMM_ARGS);
 extern "C" int paik_gemm_mfma_q8_0(PAI_GEMM_ARGS);
 extern "C" int paik_gemm_mfma_q4_k(PAI_GEMM_ARGS);
 extern "C" int paik_gemm_mfma_q6_k(PAI_GEMM_ARGS);
-extern "C" int paik_gemm_mfma(PAI_GEMM_ARGS) {
-  switch (v->type) {
-  case 8u: return paik_gemm_mfma_q8_0(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
-  case 2u: return paik_gemm_mfma_q4_0(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
-  case 12u: return paik_gemm_mfma_q4_k(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
-  case 14u: return paik_gemm_mfma_q6_k(v, m, x, y, gate, bf16, x16, x16_bytes, stream);
+extern "C" int paik_gemm_mfma_multi(PAI_GEMM_ARGS) {
+  if (count == 0u || count > (uint32_t)kGemmMats || (gate != nullptr && count != 1u))
+    return (int)hipErrorInvalidValue;
+  for (uint32_t i = 1; i < count; ++i)
+    if (vs[i]->type != vs[0]->type || vs[i]->k != vs[0]->k) return (int)hipErrorInvalidValue;
+  switch (vs[0]->type) {
+  case 8u: return paik_gemm_mfma_q8_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
+  case 2u: return paik_gemm_mfma_q4_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
+  case 12u: return paik_gemm_mfma_q4_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
+  case 14u: return paik_gemm_mfma_q6_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
   default: return (int)hipErrorInvalidValue;
   }
+}
+extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
+                              const float *gate, int bf16, void *x16, uint64_t x16_bytes,
+                              void *stream) {
+  return paik_gemm_mfma_multi(&v, &y, 1u, m, x, gate, bf16, x16, x16_bytes, stream);
+}
+extern "C" uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m) {
+  GemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.v = *v;
+  a.m = m;
+  if (m <= 32u) plan_grid(a, 256u, 32u);
+  else if (m < 256u) plan_grid(a, 256u, 128u);
+  else plan_grid(a, 128u, 256u);
+  return a.splits;
+}
+extern "C" int paik_silu_mul_inplace(float *h, const float *u, uint64_t n, void *stream) {
+  const uint64_t blocks = (n + 255u) / 256u;
+  k_silu_mul<><<<dim3((unsigned)(blocks < 4096u ? blocks : 4096u)), 256, 0, (hipStream_t)stream>>>(
+      h, u, (size_t)n);
+  return (int)hipGetLastError();
 }
 #endif

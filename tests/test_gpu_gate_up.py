@@ -111,9 +111,12 @@ def test_mfma_gate_up_unsplit_matches_composition(monkeypatch, qtype, m):
 
 
 @pytest.mark.parametrize("qtype", [12, 14])
-@pytest.mark.parametrize("m", [8, 64])
-def test_mfma_gate_up_against_f64_oracle(qtype, m):
-    n, k = 1024, 2048  # the gate launch splits over K here, the up launch does not
+@pytest.mark.parametrize("m,k", [(8, 2048), (64, 2048), (32, 4096)])
+def test_mfma_gate_up_against_f64_oracle(qtype, m, k):
+    # With 32 and 64 tokens both products split over K (few row tiles): the
+    # up product goes to the handle's workspace and a third launch forms
+    # silu(gate) * up.
+    n = 1024
     say(f"[gpu] gate_up mfma type={qtype} m={m}")
     h, g, u, bg, bu, x = run(qtype, n, k, m, 6000 + qtype + m)
     ref = ob.silu_mul(ob.qgemm_f64(qtype, n, k, bg, x).astype(np.float32),
