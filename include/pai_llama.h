@@ -46,7 +46,7 @@ pai_status_t pai_rmsnorm_f32_async(float *x, const float *delta, const float *ga
  * produces: RMSNORM then GEMM (adapters/llama/llama.c:674-693, :756-769,
  * :884-891), GEMM then ADD (:742-749, :788-795).
  *
- * ys[i] = rmsnorm(x, gamma, eps) W_i^T for count (1..4) matrices of one
+ * ys[i] = rmsnorm(x, gamma, eps) W_i^T for count (1..3) matrices of one
  * format and K (q, k, v; the output head). Each workgroup computes the
  * RMS of the whole row itself (sum of squares in double, products in the
  * reference's order, as pai_rmsnorm_f32_async), so no normalised copy of x

@@ -56,6 +56,7 @@ pai_status_t pai_rmsnorm_f32_async(float *x, const float *delta, const float *ga
  * fused in (paik_gemv_one): the RMSNorm before a projection, the residual
  * ADD after one. */
 #define PAI_FUSED_MAX 4u
+#define PAI_FUSED_NORM_MAX 3u /* matrices per fused-RMSNorm launch */
 
 static pai_status_t check_one(const pai_qmat_t *const *ws, uint32_t count, const float *x,
                               float *const *ys, const paik_qview_t **vs) {
@@ -87,6 +88,8 @@ pai_status_t pai_qgemv_rmsnorm_f32_async(const pai_qmat_t *const *ws, uint32_t c
                                          const float *x, const float *gamma, float eps,
                                          float *const *ys, void *stream) {
   const paik_qview_t *vs[PAI_FUSED_MAX];
+  if (count > PAI_FUSED_NORM_MAX)
+    return fail(PAI_ERR_INVALID_ARG, "count=%u, expected 1..%u", count, PAI_FUSED_NORM_MAX);
   TRY(check_one(ws, count, x, ys, vs));
   TRY(check_gamma(gamma, vs[0]->type, vs[0]->k));
   if (eps == 0.0f) eps = 1e-5f; /* cpu/reference/ref_ops.c:203-205 */

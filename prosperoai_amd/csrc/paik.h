@@ -70,7 +70,7 @@ int paik_gemv_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
                        uint32_t m, const float *x, float *h, void *stream);
 uint32_t paik_gemv_pair_max_k(void);
 /* One token on the integer-dot kernel with the decode step's fusions, in
- * one launch: y_i = x' W_i^T for count (1..4) matrices of one format and K,
+ * one launch: y_i = x' W_i^T for count (1..4; 1..3 with gamma) matrices of one format and K,
  * where x' = rmsnorm(x, gamma, eps) when gamma is set (one RMS per
  * workgroup; K up to paik_gemv_norm_max_k(type)) and x' = x otherwise; accum
  * set adds the products to y (each output has one writer per launch);

@@ -154,7 +154,7 @@ def test_decode_entry_points_reject_bad_arguments_before_device():
     # fused norm / residual projections: NULL arguments and matrix counts
     assert lib.pai_qgemv_rmsnorm_f32_async(None, 1, fake, fake, 0.0, fake, None) == -1
     assert lib.pai_qgemv_rmsnorm_f32_async(fake, 0, fake, fake, 0.0, fake, None) == -1
-    assert lib.pai_qgemv_rmsnorm_f32_async(fake, 5, fake, fake, 0.0, fake, None) == -1
+    assert lib.pai_qgemv_rmsnorm_f32_async(fake, 4, fake, fake, 0.0, fake, None) == -1
     assert lib.pai_qgemv_rmsnorm_gate_up_async(None, fake, fake, fake, 0.0, fake, None) == -1
     assert lib.pai_qgemv_add_f32_async(None, fake, fake, None) == -1
     assert lib.pai_qgemv_add_f32_async(fake, None, fake, None) == -1
