@@ -212,9 +212,10 @@ struct GemvArgs {
 };
 /* NORM launches take at most kMaxMats - 1 matrices and carry the RMSNorm
  * weights (K floats) in the last output slot, so the argument block keeps
- * its size (560 bytes with the launch's hidden arguments): with 16 bytes
- * more (576), every launch of the plain kernel measured 0.2-0.4 us slower
- * on the same code (the Q4_0 decode step 3160 -> 3055 GB/s). */
+ * its layout (560 bytes with the launch's hidden arguments). Measured on
+ * the Q4_0 decode step against this layout (3160 GB/s): 16 bytes more,
+ * same instructions otherwise, 3055; a compact 512-byte block (per-matrix
+ * planes and row count, shared K), 3070. */
 constexpr int kNormGammaSlot = kMaxMats - 1;
 
 /* RMSNorm of a one-token activation row held in registers (the x_load
