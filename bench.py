@@ -446,7 +446,53 @@ def cpu_baseline(pa, budget_s: float) -> dict:
             break
     bytes_step = sum(call_bytes(pa, pa.Q4_0, n, k) for _, n, k in PROJ)
     med = float(np.median(times))
+
+    def timed(fn, budget: float, least: int = 3) -> list:
+        fn()
+        ts, t_start = [], time.perf_counter()
+        while len(ts) < least or (time.perf_counter() - t_start < budget and len(ts) < 100):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return ts
+
+    # the same GEMV, rows split over every host core (a pthread wrapper
+    # around the same AVX2 row kernel; the reference itself runs one thread)
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))  # the host share of one GPU
+    orc = ob.oracle()
+
+    def mt_pass():
+        for (_, n, k), a, y in zip(PROJ, mats, ys):
+            orc.orc_opt_gemv_avx2_mt(n, k, a.ctypes.data, x.ctypes.data, y.ctypes.data, threads)
+
+    mt_times = timed(mt_pass, min(5.0, budget_s / 3))
+    mt_med = float(np.median(mt_times))
+    # the reference's int8-weight GEMM at group size 32 (the Q8_0 analogue),
+    # M=1 on the 4096 x 4096 shape of the Q8_0 configuration: w_q [K][N]
+    w8 = None
+    if r is not None:
+        n8 = k8 = 4096
+        rng = np.random.default_rng(8)
+        wq = rng.integers(-127, 128, size=(k8, n8), dtype=np.int8)
+        sc = (rng.random((k8 // 32, n8), dtype=np.float32) * 1e-3).astype(np.float32)
+        x8 = pa.normal_f32(0x8808, k8)
+        y8 = np.empty(n8, np.float32)
+        w8_times = timed(lambda: r.pai_opt_gemm_w8_f32(1, n8, k8, x8.ctypes.data, wq.ctypes.data,
+                                                       sc.ctypes.data, 32, y8.ctypes.data),
+                         min(3.0, budget_s / 5))
+        w8_med = float(np.median(w8_times))
+        q8_bytes = call_bytes(pa, pa.Q8_0, n8, k8)
+        w8 = {"GBps": round(q8_bytes / w8_med / 1e9, 2), "ms": round(w8_med * 1e3, 3),
+              "cores": 1, "sample": f"{len(w8_times)} calls of pai_opt_gemm_w8_f32, M=1, "
+                                    f"N=K=4096, group 32; GB/s counts the Q8_0 bytes of the "
+                                    f"same shape"}
     return {"value": round(bytes_step / med / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": kind,
+            "harness_parallel": {"value": round(bytes_step / mt_med / 1e9, 2), "unit": "GB/s",
+                                 "cores": threads, "kind": "port",
+                                 "sample": f"{len(mt_times)} passes, orc_opt_gemv_avx2_mt "
+                                           f"(the AVX2 row kernel, rows split over {threads} "
+                                           f"threads)"},
+            "w8_gemm_q8_0_shape": w8,
             "sample": f"{len(times)} passes over the seven Q4_0 projections of one layer "
                       f"(pai_opt_gemv_f32 on dequantized f32 [N][K], 4 B/weight touched); "
                       f"median {med * 1e3:.1f} ms/pass, min {min(times) * 1e3:.1f} ms; "
