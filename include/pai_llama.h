@@ -48,9 +48,11 @@ pai_status_t pai_rmsnorm_f32_async(float *x, const float *delta, const float *ga
  *
  * ys[i] = rmsnorm(x, gamma, eps) W_i^T for count (1..3) matrices of one
  * format and K (q, k, v; the output head). Each workgroup computes the
- * RMS of the whole row itself (sum of squares in double, products in the
- * reference's order, as pai_rmsnorm_f32_async), so no normalised copy of x
- * is written. K <= 16384 (8192 for Q8_0: one column slice); x and gamma 16-byte aligned,
+ * RMS of the whole row itself (sum of squares in double, as
+ * pai_rmsnorm_f32_async) while it forms x * gamma, and scales each finished
+ * dot product by rms; no normalised copy of x is written. Scaling the sums
+ * rather than each element moves one rounding: rel-L2 <= 1e-5 against the
+ * reference's RMSNORM then GEMM. K <= 16384 (8192 for Q8_0: one column slice); x and gamma 16-byte aligned,
  * eps = 0 meaning 1e-5. */
 pai_status_t pai_qgemv_rmsnorm_f32_async(const pai_qmat_t *const *ws, uint32_t count,
                                          const float *x, const float *gamma, float eps,

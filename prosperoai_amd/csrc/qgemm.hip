@@ -747,8 +747,9 @@ static hipError_t zero_fill(float *y, size_t count, hipStream_t s) {
 }
 
 /* Grid of a launch: tiles of RWG rows x TT tokens; K split while the grid
- * would leave most of the 256 CUs idle (at least 8 steps per split), the
- * step count per split a multiple of 4. */
+ * would leave most of the 256 CUs idle (at least 8 steps per split, or 4
+ * where there are more than two splits anyway), the step count per split a
+ * multiple of 4. */
 static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
   if (a.count <= 1u) a.tiles_n = (a.v.n + rwg - 1u) / rwg; /* else set by the caller */
   a.tiles_m = (a.m + tt - 1u) / tt;
@@ -756,6 +757,11 @@ static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
   const uint32_t nsteps = ((a.v.k >> 5) + 3u) >> 2;
   uint32_t splits = 1;
   while (tiles * splits * 2u <= 256u && nsteps / (splits * 2u) >= 8u) splits *= 2u;
+  /* Sums of more than two parts already depend on the order of the atomic
+   * adds; there the parts may be as short as 4 steps, which fills more of
+   * the chip (one or two parts stay exact and repeatable). */
+  if (splits > 2u)
+    while (tiles * splits * 2u <= 256u && nsteps / (splits * 2u) >= 4u) splits *= 2u;
   if (const char *e = getenv("PAI_GEMM_SPLITS")) {
     const int r = atoi(e);
     if (r >= 1 && r <= 64) splits = (uint32_t)r;

@@ -219,16 +219,20 @@ struct GemvArgs {
 constexpr int kNormGammaSlot = kMaxMats - 1;
 
 /* RMSNorm of a one-token activation row held in registers (the x_load
- * layout, every element of the row loaded once across the workgroup):
+ * layout, every element of the row loaded once across the workgroup),
  * rms = 1 / sqrtf((float)(sum x^2 / n) + eps) with the sum of squares in
- * double, then x = x * gamma * rms, the two products in that order
- * (pai_ref_rmsnorm_gamma_f32, cpu/reference/ref_ops.c:195-216). The double
- * sum runs lanes -> waves in a fixed order. */
-template <int NW, int XI>
-__device__ __forceinline__ void rms_apply(float4 (&va)[XI], float4 (&vb)[XI],
+ * double (pai_ref_rmsnorm_gamma_f32, cpu/reference/ref_ops.c:195-216), in
+ * two parts so that nothing waits for the reduction before the planes are
+ * built: rms_begin turns x into x * gamma and leaves each wave's partial
+ * sum of squares (lanes in a fixed order) in red[]; after the barrier that
+ * publishes the planes, rms_end adds the waves in order and forms rms,
+ * which scales every finished dot product. Against the reference's
+ * per-element (x * gamma) * rms this moves one rounding, O(2^-24)
+ * relative. */
+template <int XI>
+__device__ __forceinline__ void rms_begin(float4 (&va)[XI], float4 (&vb)[XI],
                                           const float4 (&ga)[XI], const float4 (&gb)[XI],
-                                          uint32_t n, float eps) {
-  __shared__ double red[NW];
+                                          double *red) {
   double acc = 0.0;
 #pragma unroll
   for (int it = 0; it < XI; ++it) {
@@ -243,19 +247,21 @@ __device__ __forceinline__ void rms_apply(float4 (&va)[XI], float4 (&vb)[XI],
   }
   for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = acc;
-  __syncthreads();
-  double tot = 0.0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) tot += red[w];
-  const float rms = 1.0f / sqrtf((float)(tot / (double)n) + eps);
-  auto sc = [rms](float4 x, float4 g) {
-    return make_float4(x.x * g.x * rms, x.y * g.y * rms, x.z * g.z * rms, x.w * g.w * rms);
+  auto mul = [](float4 x, float4 g) {
+    return make_float4(x.x * g.x, x.y * g.y, x.z * g.z, x.w * g.w);
   };
 #pragma unroll
   for (int it = 0; it < XI; ++it) {
-    va[it] = sc(va[it], ga[it]);
-    vb[it] = sc(vb[it], gb[it]);
+    va[it] = mul(va[it], ga[it]);
+    vb[it] = mul(vb[it], gb[it]);
   }
+}
+template <int NW>
+__device__ __forceinline__ float rms_end(const double *red, uint32_t n, float eps) {
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) tot += red[w];
+  return 1.0f / sqrtf((float)(tot / (double)n) + eps);
 }
 
 /* Weight loads of a block are issued for all its lanes and rows with
@@ -351,9 +357,11 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 #pragma unroll
   for (int p = 0; p < PD; ++p) load_block((uint32_t)p, buf[p]);
 
-  if constexpr (NORM) rms_apply<NW, XI>(xa, xb, ga, gb, v.k, a.eps);
+  __shared__ double red[NORM ? NW : 1];
+  if constexpr (NORM) rms_begin<XI>(xa, xb, ga, gb, red);
   x_planes<MT, XI>(nsc, xa, xb, xp, xf);
   __syncthreads();
+  const float rms = NORM ? rms_end<NW>(red, v.k, a.eps) : 1.0f;
 
   float acc[U][MT];
 #pragma unroll
@@ -398,8 +406,12 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
       for (int p = 0; p < UR; ++p)
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const float sg = group_sum<64>(acc[2 * p][t]);
-          const float su = group_sum<64>(acc[2 * p + 1][t]);
+          float sg = group_sum<64>(acc[2 * p][t]);
+          float su = group_sum<64>(acc[2 * p + 1][t]);
+          if constexpr (NORM) {
+            sg *= rms;
+            su *= rms;
+          }
           acc[2 * p][t] = 0.0f;
           acc[2 * p + 1][t] = 0.0f;
           const uint32_t row = row0 + (uint32_t)p;
@@ -414,7 +426,8 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
       for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          const float sum = group_sum<64>(acc[u][t]);
+          float sum = group_sum<64>(acc[u][t]);
+          if constexpr (NORM) sum *= rms;
           acc[u][t] = 0.0f;
           const uint32_t row = row0 + (uint32_t)u;
           if (lane == (uint32_t)(u * MT + t) && row < r_end && (uint32_t)t < ntok) {

@@ -99,8 +99,10 @@ def ptr_array(ptrs):
 @pytest.mark.parametrize("qtype,k,n", FUSED_CASES)
 def test_fused_rmsnorm_projections(qtype, k, n):
     """rmsnorm(x) W_i^T in one launch (one, then three matrices) against the
-    oracle's RMSNorm followed by its sequential qgemm, and bit for bit
-    against pai_rmsnorm_f32_async followed by pai_qgemm_f32_multi_async."""
+    oracle's RMSNorm followed by its sequential qgemm (f32 bar), and within
+    1e-6 of pai_rmsnorm_f32_async followed by pai_qgemm_f32_multi_async (the
+    fused kernel scales the finished dot products by rms instead of each
+    element: one rounding moved)."""
     say(f"[gpu] fused rmsnorm+gemv type={qtype} k={k} n={n}")
     rng = np.random.default_rng(k + n)
     x = (rng.standard_normal(k) * 3).astype(np.float32)
@@ -128,7 +130,7 @@ def test_fused_rmsnorm_projections(qtype, k, n):
             got = ys[i].download(ni)
             want = ob.qgemm_seq(qtype, ni, k, blocks, xn.reshape(1, k)).reshape(ni)
             assert rel_l2(got, want) <= 1e-5, (count, i)
-            assert np.array_equal(got.view(np.uint32), ys2[i].download(ni).view(np.uint32))
+            assert rel_l2(got, ys2[i].download(ni)) <= 1e-6, (count, i)
 
 
 @pytest.mark.parametrize("qtype,k,n", FUSED_CASES)
