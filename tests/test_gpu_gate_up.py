@@ -124,6 +124,27 @@ def test_mfma_gate_up_against_f64_oracle(qtype, m, k):
     assert rel_l2(h, ref) <= TOL_F16
 
 
+def test_mfma_gate_up_split_workspace_regrows():
+    """The split-K gate/up path keeps the up product in a workspace owned by
+    the up matrix's handle; calls with more tokens on the same handles grow
+    it, and every call stays within the 16-bit bar of the f64 oracle."""
+    from prosperoai_amd.hipmem import DeviceBuffer, Stream
+    qtype, n, k = 12, 1024, 4096
+    say("[gpu] gate_up split workspace regrow")
+    bg, bu = weights(qtype, n, k, 7100), weights(qtype, n, k, 7101)
+    wg, wu = pa.QMat(qtype, n, k, bg), pa.QMat(qtype, n, k, bu)
+    st = Stream()
+    for m in (16, 48, 32):
+        x = pa.normal_f32(7102 + m, m * k).reshape(m, k)
+        xd, hd = DeviceBuffer.from_array(x), DeviceBuffer(m * n * 4)
+        pa.gate_up_async(wg, wu, xd.ptr, hd.ptr, m, 0, st.handle)
+        st.synchronize()
+        ref = ob.silu_mul(ob.qgemm_f64(qtype, n, k, bg, x).astype(np.float32),
+                          ob.qgemm_f64(qtype, n, k, bu, x).astype(np.float32))
+        assert rel_l2(hd.download((m, n)), ref) <= TOL_F16, m
+    st.destroy()
+
+
 def test_gate_up_argument_errors():
     from prosperoai_amd.hipmem import DeviceBuffer
     say("[gpu] gate_up errors")

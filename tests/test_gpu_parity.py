@@ -355,13 +355,17 @@ def test_multi_matches_separate_calls(qtype, m):
 
 @pytest.mark.parametrize("qtype", [12, 14])
 @pytest.mark.parametrize("m,k", [(32, 4096), (64, 2048)])
-def test_multi_mfma_split_k_against_oracle(qtype, m, k):
+@pytest.mark.parametrize("bf16", [False, True])
+def test_multi_mfma_split_k_against_oracle(qtype, m, k, bf16):
     """q/k/v-shaped matrices on the MFMA path in one launch whose row tiles
     are few, so K is split over workgroups (f32 atomic partial sums): each
-    output within the 16-bit bar of the f64 oracle."""
+    output within the 16-bit bar (fp16 or bf16 operands) of the f64
+    oracle."""
     from prosperoai_amd.hipmem import DeviceBuffer, Stream
     shapes = [512, 128, 128]
-    say(f"[gpu] multi mfma split-k type={qtype} m={m} k={k}")
+    say(f"[gpu] multi mfma split-k type={qtype} m={m} k={k} bf16={bf16}")
+    flags = pa.FLAG_MFMA_BF16 if bf16 else 0
+    tol = TOL_BF16 if bf16 else TOL_F16
     mats, blocks = [], []
     for i, n in enumerate(shapes):
         b = weights(qtype, n, k, 1900 + 10 * i + qtype)
@@ -372,11 +376,11 @@ def test_multi_mfma_split_k_against_oracle(qtype, m, k):
     yd = [DeviceBuffer(m * n * 4) for n in shapes]
     st = Stream()
     for rep in range(2):  # the second call reuses the zero-filled outputs' buffers
-        pa.gemm_multi_async(mats, xd.ptr, [y.ptr for y in yd], m, 0, st.handle)
+        pa.gemm_multi_async(mats, xd.ptr, [y.ptr for y in yd], m, flags, st.handle)
         st.synchronize()
         for w, b, y, n in zip(mats, blocks, yd, shapes):
             got = y.download((m, n))
-            assert rel_l2(got, ob.qgemm_f64(qtype, n, k, b, x)) <= TOL_F16, (rep, n)
+            assert rel_l2(got, ob.qgemm_f64(qtype, n, k, b, x)) <= tol, (rep, n)
     st.destroy()
 
 
