@@ -452,6 +452,7 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
    * every store or atomic add of a wave covers RW consecutive outputs of
    * one token. */
   const bool split_k = a.splits > 1u;
+  const bool gated = a.gate != nullptr && !split_k;
   float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW; /* tokens per read-out instruction */
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
@@ -464,15 +465,30 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
         *reinterpret_cast<float4 *>(&Ts[r * kTP + 32 * i + 8 * q + 4 * g]) =
             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                         acc[i][j][4 * q + 3]);
-#pragma unroll 4
-    for (int t = 0; t < 32; t += TPI) {
-      const int tt = t + lane / RW;
+    /* With the silu epilogue, the fragment's gate values are requested
+     * together (clamped addresses) before its stores: one round trip per
+     * fragment instead of one per store (the gate may be the output itself;
+     * every element is read before this thread writes it). */
+    constexpr int NQ = 32 / TPI;
+    float gv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) gv[q] = 0.0f;
+    if (gated) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t tok = min(m0 + (uint32_t)(32 * j + q * TPI + lane / RW), a.m - 1u);
+        gv[q] = a.gate[(size_t)tok * v.n + min(orow, v.n - 1u)];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int tt = q * TPI + lane / RW;
       const float val = Ts[tt * kTP + lane % RW];
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
         if (split_k) unsafeAtomicAdd(a.y + at, val);
-        else if (a.gate != nullptr) a.y[at] = silu_mul(a.gate[at], val);
+        else if (gated) a.y[at] = silu_mul(gv[q], val);
         else a.y[at] = val;
       }
     }
@@ -694,6 +710,7 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
   __syncthreads();
 
   const bool split_k = a.splits > 1u;
+  const bool gated = a.gate != nullptr && !split_k;
   float *Ts = reinterpret_cast<float *>(Xb) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW;
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
@@ -706,15 +723,30 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
         *reinterpret_cast<float4 *>(&Ts[r * kTP + 32 * i + 8 * q + 4 * g]) =
             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                         acc[i][j][4 * q + 3]);
-#pragma unroll 4
-    for (int t = 0; t < 32; t += TPI) {
-      const int tt = t + lane / RW;
+    /* With the silu epilogue, the fragment's gate values are requested
+     * together (clamped addresses) before its stores: one round trip per
+     * fragment instead of one per store (the gate may be the output itself;
+     * every element is read before this thread writes it). */
+    constexpr int NQ = 32 / TPI;
+    float gv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) gv[q] = 0.0f;
+    if (gated) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t tok = min(m0 + (uint32_t)(32 * j + q * TPI + lane / RW), a.m - 1u);
+        gv[q] = a.gate[(size_t)tok * v.n + min(orow, v.n - 1u)];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int tt = q * TPI + lane / RW;
       const float val = Ts[tt * kTP + lane % RW];
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
         if (split_k) unsafeAtomicAdd(ybase + at, val);
-        else if (a.gate != nullptr) ybase[at] = silu_mul(a.gate[at], val);
+        else if (gated) ybase[at] = silu_mul(gv[q], val);
         else ybase[at] = val;
       }
     }
