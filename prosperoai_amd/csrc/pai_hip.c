@@ -517,22 +517,26 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
     const int e = paik_gemv_silu_mul(&w_gate->view, &w_up->view, (uint32_t)m, x, h, s);
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
-  /* The gate product lands in h. When the up product splits over K (few
-   * tiles: batched decode), it lands in a workspace and a third launch
-   * forms silu(gate) * up; otherwise the up product's epilogue does that
-   * in place (whole sums, no split). */
-  st = launch_mfma(w_gate, m, x, h, NULL, flags, s);
-  if (st != PAI_OK) return st;
+  /* When the up product would split over K (few tiles: batched decode),
+   * gate and up run as one two-matrix launch (gate into h, up into a
+   * workspace owned by the up handle; one activation conversion) and a
+   * third launch forms silu(gate) * up. Otherwise the gate product lands in
+   * h and the up product's epilogue forms silu(gate) * up in place (whole
+   * sums, no split). */
   if (paik_gemm_x16_splits(&w_up->view, (uint32_t)(m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS)) > 1u &&
       getenv("PAI_GEMM_NO_X16") == NULL) {
     float *u = ywork_workspace(w_up, m, s);
     if (u != NULL) {
-      st = launch_mfma(w_up, m, x, u, NULL, flags, s);
+      const pai_qmat_t *pair[2] = {w_gate, w_up};
+      float *outs[2] = {h, u};
+      st = launch_mfma_multi(pair, 2u, m, x, outs, flags, s);
       if (st != PAI_OK) return st;
       const int e = paik_silu_mul_inplace(h, u, m * w_up->n, s);
       return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
     }
   }
+  st = launch_mfma(w_gate, m, x, h, NULL, flags, s);
+  if (st != PAI_OK) return st;
   return launch_mfma(w_up, m, x, h, h, flags, s);
 }
 
