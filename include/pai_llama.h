@@ -188,7 +188,13 @@ pai_status_t pai_llama_kv_write(pai_llama_t *m, uint32_t layer, uint32_t pos0, u
 /* One greedy decode step: token at position pos, the cache holding
  * positions 0..pos-1. Stores the step's keys and values at pos, leaves the
  * logits in the model (pai_llama_logits) and writes the argmax to *next.
- * logits (host, vocab floats) may be NULL. Synchronous. */
+ * logits (host, vocab floats) may be NULL. Synchronous.
+ * The step is the embedding row, then per layer: RMSNorm + q/k/v in one
+ * launch (pai_qgemv_rmsnorm_f32_async), RoPE + cache append + attention in
+ * two (pai_attention_decode_rope_async), the o projection added into the
+ * residual (pai_qgemv_add_f32_async), RMSNorm + gate/up + SiLU-mul in one
+ * (pai_qgemv_rmsnorm_gate_up_async) and down added into the residual; then
+ * the output norm + head in one launch and the two-launch argmax. */
 pai_status_t pai_llama_decode(pai_llama_t *m, uint32_t token, uint32_t pos, uint32_t *next,
                               float *logits);
 
