@@ -261,6 +261,10 @@ struct GemmArgs {
   uint32_t tile_end[kGemmMats];
   paik_qview_t mv[kGemmMats];
   float *my[kGemmMats];
+  /* split launches with a workspace: part p of matrix i's output goes to
+   * part + splits * m * (rows of matrices 0..i-1) + p * m * n_i, and a
+   * reduce launch sums the parts in order (no zero fill, no atomics) */
+  float *part;
 };
 
 /* Tile shapes: TT tokens x RWG weight rows, NW waves of RWG/NW rows; XB
@@ -453,6 +457,7 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
    * one token. */
   const bool split_k = a.splits > 1u;
   const bool gated = a.gate != nullptr && !split_k;
+  float *const pbase = a.part != nullptr ? a.part + (size_t)split * a.m * v.n : nullptr;
   float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW; /* tokens per read-out instruction */
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
@@ -487,7 +492,8 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
-        if (split_k) unsafeAtomicAdd(a.y + at, val);
+        if (pbase != nullptr) pbase[at] = val;
+        else if (split_k) unsafeAtomicAdd(a.y + at, val);
         else if (gated) a.y[at] = silu_mul(gv[q], val);
         else a.y[at] = val;
       }
@@ -548,14 +554,17 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
   /* the matrix owning row tile tn (workgroup-uniform) */
   paik_qview_t v = a.v;
   float *ybase = a.y;
-  uint32_t tl = tn;
+  uint32_t tl = tn, rows_before = 0, cum = 0; /* rows of the matrices ahead of this one */
 #pragma unroll
-  for (int i = 1; i < kGemmMats; ++i)
+  for (int i = 1; i < kGemmMats; ++i) {
+    cum += a.mv[i - 1].n;
     if ((uint32_t)i < a.count && tn >= a.tile_end[i - 1]) {
       v = a.mv[i];
       ybase = a.my[i];
       tl = tn - a.tile_end[i - 1];
+      rows_before = cum;
     }
+  }
   const uint32_t n0 = tl * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
   const uint32_t s0 = split * a.steps_per_split;
@@ -711,6 +720,9 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
 
   const bool split_k = a.splits > 1u;
   const bool gated = a.gate != nullptr && !split_k;
+  float *const pbase = a.part != nullptr ? a.part + (size_t)a.splits * a.m * rows_before +
+                                                (size_t)split * a.m * v.n
+                                          : nullptr;
   float *Ts = reinterpret_cast<float *>(Xb) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW;
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
@@ -745,7 +757,8 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm_x16(GemmArgs a) {
       const uint32_t tok = m0 + (uint32_t)(32 * j + tt);
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
-        if (split_k) unsafeAtomicAdd(ybase + at, val);
+        if (pbase != nullptr) pbase[at] = val;
+        else if (split_k) unsafeAtomicAdd(ybase + at, val);
         else if (gated) ybase[at] = silu_mul(gv[q], val);
         else ybase[at] = val;
       }
@@ -805,9 +818,61 @@ static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
   a.per_xcd = (tiles * a.splits + kXcds - 1u) / kXcds;
 }
 
+/* The split parts summed in part order (0, 1, ...): y_i[e] = sum_p
+ * part[base_i + p * len_i + e], base_i = splits * (len_0 + ... + len_{i-1}),
+ * len_i = m * n_i; e runs over all matrices' outputs back to back. */
+struct ReduceArgs {
+  const float *part;
+  float *y[kGemmMats];
+  size_t end[kGemmMats]; /* cumulative output lengths */
+  uint32_t count, splits;
+};
+template <int = 0>
+__global__ void __launch_bounds__(256) k_split_reduce(ReduceArgs r) {
+  const size_t total = r.end[r.count - 1];
+  for (size_t e = (size_t)blockIdx.x * 256u + threadIdx.x; e < total; e += (size_t)gridDim.x * 256u) {
+    uint32_t i = 0;
+    size_t start = 0;
+#pragma unroll
+    for (int j = 1; j < kGemmMats; ++j)
+      if ((uint32_t)j < r.count && e >= r.end[j - 1]) {
+        i = (uint32_t)j;
+        start = r.end[j - 1];
+      }
+    const size_t len = r.end[i] - start, off = e - start;
+    const float *src = r.part + (size_t)r.splits * start + off;
+    float acc = src[0];
+    for (uint32_t p = 1; p < r.splits; ++p) acc += src[(size_t)p * len];
+    float *yi = r.y[0];
+#pragma unroll
+    for (int j = 1; j < kGemmMats; ++j)
+      if ((uint32_t)j == i) yi = r.y[j];
+    yi[off] = acc;
+  }
+}
+
+static hipError_t launch_reduce(float *part, float *const *ys, const uint32_t *ns, uint32_t count,
+                                uint32_t m, uint32_t splits, hipStream_t s) {
+  ReduceArgs r;
+  memset(&r, 0, sizeof r);
+  r.part = part;
+  size_t cum = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    r.y[i] = ys[i];
+    cum += (size_t)m * ns[i];
+    r.end[i] = cum;
+  }
+  r.count = count;
+  r.splits = splits;
+  const size_t blocks = (cum + 255u) / 256u;
+  k_split_reduce<><<<dim3((unsigned)(blocks < 4096u ? blocks : 4096u)), 256, 0, s>>>(r);
+  return hipGetLastError();
+}
+
 template <class F, int TT, int NW, int RWG, int XB>
 static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, float *y,
-                            const float *gate, bool bf16, hipStream_t s) {
+                            const float *gate, bool bf16, float *part, size_t part_bytes,
+                            hipStream_t s) {
   GemmArgs a;
   memset(&a, 0, sizeof a);
   a.v = v;
@@ -817,20 +882,27 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
   a.m = m;
   plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 4u);
-  if (a.splits > 1u) {
+  const bool parts = a.splits > 1u && part != nullptr &&
+                     (size_t)a.splits * m * v.n * 4u <= part_bytes;
+  if (parts) {
+    a.part = part;
+  } else if (a.splits > 1u) {
     const hipError_t e = zero_fill(y, (size_t)m * v.n, s);
     if (e != hipSuccess) return e;
   }
   const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
   if (bf16) k_gemm<F, true, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
   else k_gemm<F, false, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
-  return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !parts) return e;
+  const uint32_t n = v.n;
+  return launch_reduce(part, &y, &n, 1u, m, a.splits, s);
 }
 
 template <class F, int TT, int NW, int RWG>
 static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                              uint32_t m, const float *x, uint16_t *x16, const float *gate,
-                             bool bf16, hipStream_t s) {
+                             bool bf16, float *part, size_t part_bytes, hipStream_t s) {
   const paik_qview_t &v = *vs[0];
   const size_t n4 = (size_t)m * v.k / 4u;
   const size_t blocks = (n4 + 255u) / 256u;
@@ -856,7 +928,17 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
   a.tiles_n = tiles;
   plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 2u);
-  if (a.splits > 1u) {
+  size_t rows = 0;
+  uint32_t ns[kGemmMats];
+  for (uint32_t i = 0; i < count; ++i) {
+    ns[i] = vs[i]->n;
+    rows += vs[i]->n;
+  }
+  const bool parts = a.splits > 1u && part != nullptr &&
+                     (size_t)a.splits * m * rows * 4u <= part_bytes;
+  if (parts) {
+    a.part = part;
+  } else if (a.splits > 1u) {
     for (uint32_t i = 0; i < count; ++i) {
       e = zero_fill(ys[i], (size_t)m * vs[i]->n, s);
       if (e != hipSuccess) return e;
@@ -865,13 +947,16 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
   const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
   if (bf16) k_gemm_x16<F, true, TT, NW, RWG><<<grid, block, 0, s>>>(a);
   else k_gemm_x16<F, false, TT, NW, RWG><<<grid, block, 0, s>>>(a);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess || !parts) return e;
+  return launch_reduce(part, ys, ns, count, m, a.splits, s);
 }
 
 template <class F>
 static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                               uint32_t m, const float *x, const float *gate, bool bf16,
-                              uint16_t *x16, size_t x16_bytes, hipStream_t s) {
+                              uint16_t *x16, size_t x16_bytes, float *part, size_t part_bytes,
+                              hipStream_t s) {
   const paik_qview_t &v = *vs[0];
   /* token blocks whose activations span less than 2^31 bytes (32-bit
    * buffer offsets) and, on the 16-bit path, fit the workspace */
@@ -895,14 +980,20 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
      * matrices in one launch; the register-staged path one per matrix. */
     hipError_t e = hipSuccess;
     if (use16) {
-      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, s)
-          : mt < 256u ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, s)
-                      : launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, s);
+      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+                                                   part_bytes, s)
+          : mt < 256u ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+                                                   part_bytes, s)
+                      : launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+                                                   part_bytes, s);
     } else {
       for (uint32_t i = 0; i < count && e == hipSuccess; ++i)
-        e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, s)
-            : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, s)
-                        : launch_tt<F, 256, 4, 128, 1>(*vs[i], mt, xt, yt[i], gt, bf16, s);
+        e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, part,
+                                                       part_bytes, s)
+            : mt < 256u ? launch_tt<F, 128, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, part,
+                                                       part_bytes, s)
+                        : launch_tt<F, 256, 4, 128, 1>(*vs[i], mt, xt, yt[i], gt, bf16, part,
+                                                       part_bytes, s);
     }
     if (e != hipSuccess) return e;
   }
@@ -927,11 +1018,13 @@ using namespace paik;
  * compile in parallel; the unit without PAI_GEMM_FMT holds the dispatcher. */
 #define PAI_GEMM_ARGS                                                                         \
   const paik_qview_t *const *vs, float *const *ys, uint32_t count, uint32_t m, const float *x, \
-      const float *gate, int bf16, void *x16, uint64_t x16_bytes, void *stream
+      const float *gate, int bf16, void *x16, uint64_t x16_bytes, void *part,                  \
+      uint64_t part_bytes, void *stream
 #ifdef PAI_GEMM_FMT
 extern "C" int PAI_GEMM_ENTRY(PAI_GEMM_ARGS) {
   return (int)launch_gemm<PAI_GEMM_FMT>(vs, ys, count, m, x, gate, bf16 != 0,
                                         static_cast<uint16_t *>(x16), (size_t)x16_bytes,
+                                        static_cast<float *>(part), (size_t)part_bytes,
                                         (hipStream_t)stream);
 }
 #else
@@ -945,17 +1038,21 @@ extern "C" int paik_gemm_mfma_multi(PAI_GEMM_ARGS) {
   for (uint32_t i = 1; i < count; ++i)
     if (vs[i]->type != vs[0]->type || vs[i]->k != vs[0]->k) return (int)hipErrorInvalidValue;
   switch (vs[0]->type) {
-  case 8u: return paik_gemm_mfma_q8_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
-  case 2u: return paik_gemm_mfma_q4_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
-  case 12u: return paik_gemm_mfma_q4_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
-  case 14u: return paik_gemm_mfma_q6_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, stream);
+  case 8u: return paik_gemm_mfma_q8_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
+                                   part_bytes, stream);
+  case 2u: return paik_gemm_mfma_q4_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
+                                   part_bytes, stream);
+  case 12u: return paik_gemm_mfma_q4_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
+                                   part_bytes, stream);
+  case 14u: return paik_gemm_mfma_q6_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
+                                   part_bytes, stream);
   default: return (int)hipErrorInvalidValue;
   }
 }
 extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
                               const float *gate, int bf16, void *x16, uint64_t x16_bytes,
                               void *stream) {
-  return paik_gemm_mfma_multi(&v, &y, 1u, m, x, gate, bf16, x16, x16_bytes, stream);
+  return paik_gemm_mfma_multi(&v, &y, 1u, m, x, gate, bf16, x16, x16_bytes, nullptr, 0u, stream);
 }
 extern "C" uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m) {
   GemmArgs a;
@@ -966,6 +1063,24 @@ extern "C" uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m) {
   else if (m < 256u) plan_grid(a, 256u, 128u);
   else plan_grid(a, 128u, 256u);
   return a.splits;
+}
+extern "C" uint64_t paik_gemm_part_bytes(const paik_qview_t *const *vs, uint32_t count,
+                                         uint32_t m) {
+  if (m > 1024u) m = 1024u; /* the largest token block of the 16-bit path */
+  GemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.v = *vs[0];
+  a.m = m;
+  a.count = count;
+  const uint32_t tt = m <= 32u ? 32u : m < 256u ? 128u : 256u;
+  const uint32_t rwg = m < 256u ? 256u : 128u;
+  uint64_t rows = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    a.tiles_n += (vs[i]->n + rwg - 1u) / rwg;
+    rows += vs[i]->n;
+  }
+  plan_grid(a, rwg, tt);
+  return a.splits > 1u ? (uint64_t)a.splits * m * rows * 4u : 0u;
 }
 extern "C" int paik_silu_mul_inplace(float *h, const float *u, uint64_t n, void *stream) {
   const uint64_t blocks = (n + 255u) / 256u;
