@@ -358,9 +358,9 @@ def test_multi_matches_separate_calls(qtype, m):
 @pytest.mark.parametrize("bf16", [False, True])
 def test_multi_mfma_split_k_against_oracle(qtype, m, k, bf16):
     """q/k/v-shaped matrices on the MFMA path in one launch whose row tiles
-    are few, so K is split over workgroups (f32 atomic partial sums): each
-    output within the 16-bit bar (fp16 or bf16 operands) of the f64
-    oracle."""
+    are few, so K is split over workgroups (parts summed in a fixed order):
+    each output within the 16-bit bar (fp16 or bf16 operands) of the f64
+    oracle, and a second call equal to the first bit for bit."""
     from prosperoai_amd.hipmem import DeviceBuffer, Stream
     shapes = [512, 128, 128]
     say(f"[gpu] multi mfma split-k type={qtype} m={m} k={k} bf16={bf16}")
@@ -375,12 +375,18 @@ def test_multi_mfma_split_k_against_oracle(qtype, m, k, bf16):
     xd = DeviceBuffer.from_array(x)
     yd = [DeviceBuffer(m * n * 4) for n in shapes]
     st = Stream()
-    for rep in range(2):  # the second call reuses the zero-filled outputs' buffers
+    first = []
+    for rep in range(2):
         pa.gemm_multi_async(mats, xd.ptr, [y.ptr for y in yd], m, flags, st.handle)
         st.synchronize()
-        for w, b, y, n in zip(mats, blocks, yd, shapes):
+        for i, (w, b, y, n) in enumerate(zip(mats, blocks, yd, shapes)):
             got = y.download((m, n))
             assert rel_l2(got, ob.qgemm_f64(qtype, n, k, b, x)) <= tol, (rep, n)
+            # the parts are summed in a fixed order: calls repeat bit for bit
+            if rep == 0:
+                first.append(got)
+            else:
+                assert np.array_equal(got.view(np.uint32), first[i].view(np.uint32)), n
     st.destroy()
 
 
