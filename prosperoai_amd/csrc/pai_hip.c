@@ -30,10 +30,6 @@ struct pai_qmat {
    * guarded by g_x16_lock */
   void *x16;
   uint64_t x16_bytes;
-  /* the up product of a split-K gate/up call (see ywork_workspace); same
-   * lock */
-  void *yw;
-  uint64_t yw_bytes;
   /* the split parts of MFMA launches led by this handle (see part_workspace) */
   void *pw;
   uint64_t pw_bytes;
@@ -323,7 +319,6 @@ __attribute__((visibility("hidden"))) pai_status_t pai__ready(void) { return ens
 pai_status_t pai_qmat_free(pai_qmat_t *w) {
   if (w == NULL) return PAI_OK;
   if (w->x16 != NULL) (void)hipFree(w->x16);
-  if (w->yw != NULL) (void)hipFree(w->yw);
   if (w->pw != NULL) (void)hipFree(w->pw);
   hipError_t e = hipFree(w->dev);
   free(w);
@@ -413,18 +408,6 @@ static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint
   return p;
 }
 
-/* m x n floats for the up product of a split-K gate/up call, owned by the
- * up matrix's handle; NULL when it cannot be had (inside a capture). */
-static float *ywork_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s) {
-  pai_qmat_t *w = (pai_qmat_t *)cw;
-  const uint64_t want = m * w->n * 4u;
-  uint64_t have = 0;
-  pthread_mutex_lock(&g_x16_lock);
-  void *p = grow_workspace(&w->yw, &w->yw_bytes, want, s, &have);
-  pthread_mutex_unlock(&g_x16_lock);
-  return have >= want ? (float *)p : NULL;
-}
-
 /* The split parts of a multi-matrix MFMA launch (matrices vs sharing x,
  * m tokens), owned by the first matrix's handle: parts summed in a fixed
  * order by one reduce launch, in place of a zero fill per matrix and
@@ -457,7 +440,7 @@ static pai_status_t launch_mfma_multi(const pai_qmat_t *const *ws, uint32_t coun
   for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
   void *part = gate != NULL ? NULL : part_workspace(ws[0], vs, count, m, s, &pb);
   const int e = paik_gemm_mfma_multi(vs, ys, count, (uint32_t)m, x, gate,
-                                     (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, part, pb, s);
+                                     (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, part, pb, 0, s);
   return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
 }
 
@@ -540,20 +523,23 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
   /* When the up product would split over K (few tiles: batched decode),
-   * gate and up run as one two-matrix launch (gate into h, up into a
-   * workspace owned by the up handle; one activation conversion) and a
-   * third launch forms silu(gate) * up. Otherwise the gate product lands in
-   * h and the up product's epilogue forms silu(gate) * up in place (whole
-   * sums, no split). */
-  if (paik_gemm_x16_splits(&w_up->view, (uint32_t)(m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS)) > 1u &&
-      getenv("PAI_GEMM_NO_X16") == NULL) {
-    float *u = ywork_workspace(w_up, m, s);
-    if (u != NULL) {
-      const pai_qmat_t *pair[2] = {w_gate, w_up};
-      float *outs[2] = {h, u};
-      st = launch_mfma_multi(pair, 2u, m, x, outs, NULL, flags, s);
-      if (st != PAI_OK) return st;
-      const int e = paik_silu_mul_inplace(h, u, m * w_up->n, s);
+   * gate and up run as one two-matrix launch whose split parts go to a
+   * workspace, and the reduce launch that sums them forms silu(gate) * up.
+   * Otherwise (or without the workspaces, inside a capture) the gate
+   * product lands in h and the up product's epilogue forms silu(gate) * up
+   * in place (whole sums, no split). */
+  if (m <= PAI_X16_TOKENS && getenv("PAI_GEMM_NO_X16") == NULL &&
+      paik_gemm_x16_splits(&w_up->view, (uint32_t)m) > 1u) {
+    uint64_t wb = 0, pb = 0;
+    void *x16 = x16_workspace(w_gate, m, s, &wb);
+    const paik_qview_t *vs[2] = {&w_gate->view, &w_up->view};
+    const uint64_t need = paik_gemm_part_bytes(vs, 2u, (uint32_t)m);
+    void *part = part_workspace(w_gate, vs, 2u, m, s, &pb);
+    if (x16 != NULL && wb >= m * w_gate->k * 2u && part != NULL && need > 0u && pb >= need) {
+      float *outs[2] = {h, h};
+      const int e = paik_gemm_mfma_multi(vs, outs, 2u, (uint32_t)m, x, NULL,
+                                         (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, part, pb,
+                                         1, s);
       return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
     }
   }

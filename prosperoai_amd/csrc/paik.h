@@ -126,16 +126,19 @@ int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
  * launch on the 16-bit path (y_i = x W_i^T; gate only with count 1). A
  * launch split over K with part_bytes >= paik_gemm_part_bytes() stores each
  * part in `part` and sums them in a fixed order (a second launch);
- * otherwise it zero-fills y and adds the parts with atomics. */
+ * otherwise it zero-fills y and adds the parts with atomics. silu_pair:
+ * vs = {gate, up} of one shape, and the second launch writes
+ * ys[0] = silu(x W_gate^T) * (x W_up^T) (needs the parts: a split launch, a
+ * large enough part workspace and the 16-bit path for all m tokens). */
 int paik_gemm_mfma_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                          uint32_t m, const float *x, const float *gate, int bf16, void *x16,
-                         uint64_t x16_bytes, void *part, uint64_t part_bytes, void *stream);
+                         uint64_t x16_bytes, void *part, uint64_t part_bytes, int silu_pair,
+                         void *stream);
 /* Workspace bytes the split parts of such a launch need (0: no split). */
 uint64_t paik_gemm_part_bytes(const paik_qview_t *const *vs, uint32_t count, uint32_t m);
 /* K parts a 16-bit-path launch of m tokens (no gate) splits into. */
 uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m);
-/* h = silu(h) * u over n floats. */
-int paik_silu_mul_inplace(float *h, const float *u, uint64_t n, void *stream);
+
 
 #ifdef __cplusplus
 }

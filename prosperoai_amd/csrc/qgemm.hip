@@ -826,9 +826,23 @@ struct ReduceArgs {
   float *y[kGemmMats];
   size_t end[kGemmMats]; /* cumulative output lengths */
   uint32_t count, splits;
+  uint32_t silu; /* gate/up pair: y[0][e] = silu(sum of matrix 0) * (sum of matrix 1) */
 };
 template <int = 0>
 __global__ void __launch_bounds__(256) k_split_reduce(ReduceArgs r) {
+  if (r.silu != 0u) { /* two matrices of equal length, one output */
+    const size_t len = r.end[0];
+    for (size_t e = (size_t)blockIdx.x * 256u + threadIdx.x; e < len; e += (size_t)gridDim.x * 256u) {
+      const float *g = r.part + e, *u = r.part + (size_t)r.splits * len + e;
+      float sg = g[0], su = u[0];
+      for (uint32_t p = 1; p < r.splits; ++p) {
+        sg += g[(size_t)p * len];
+        su += u[(size_t)p * len];
+      }
+      r.y[0][e] = silu_mul(sg, su);
+    }
+    return;
+  }
   const size_t total = r.end[r.count - 1];
   for (size_t e = (size_t)blockIdx.x * 256u + threadIdx.x; e < total; e += (size_t)gridDim.x * 256u) {
     uint32_t i = 0;
@@ -852,10 +866,11 @@ __global__ void __launch_bounds__(256) k_split_reduce(ReduceArgs r) {
 }
 
 static hipError_t launch_reduce(float *part, float *const *ys, const uint32_t *ns, uint32_t count,
-                                uint32_t m, uint32_t splits, hipStream_t s) {
+                                uint32_t m, uint32_t splits, hipStream_t s, bool silu = false) {
   ReduceArgs r;
   memset(&r, 0, sizeof r);
   r.part = part;
+  r.silu = silu ? 1u : 0u;
   size_t cum = 0;
   for (uint32_t i = 0; i < count; ++i) {
     r.y[i] = ys[i];
@@ -902,7 +917,8 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
 template <class F, int TT, int NW, int RWG>
 static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                              uint32_t m, const float *x, uint16_t *x16, const float *gate,
-                             bool bf16, float *part, size_t part_bytes, hipStream_t s) {
+                             bool bf16, float *part, size_t part_bytes, bool silu_pair,
+                             hipStream_t s) {
   const paik_qview_t &v = *vs[0];
   const size_t n4 = (size_t)m * v.k / 4u;
   const size_t blocks = (n4 + 255u) / 256u;
@@ -936,6 +952,7 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
   }
   const bool parts = a.splits > 1u && part != nullptr &&
                      (size_t)a.splits * m * rows * 4u <= part_bytes;
+  if (silu_pair && !parts) return hipErrorInvalidValue; /* the caller checks first */
   if (parts) {
     a.part = part;
   } else if (a.splits > 1u) {
@@ -949,14 +966,14 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
   else k_gemm_x16<F, false, TT, NW, RWG><<<grid, block, 0, s>>>(a);
   e = hipGetLastError();
   if (e != hipSuccess || !parts) return e;
-  return launch_reduce(part, ys, ns, count, m, a.splits, s);
+  return launch_reduce(part, ys, ns, count, m, a.splits, s, silu_pair);
 }
 
 template <class F>
 static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                               uint32_t m, const float *x, const float *gate, bool bf16,
                               uint16_t *x16, size_t x16_bytes, float *part, size_t part_bytes,
-                              hipStream_t s) {
+                              bool silu_pair, hipStream_t s) {
   const paik_qview_t &v = *vs[0];
   /* token blocks whose activations span less than 2^31 bytes (32-bit
    * buffer offsets) and, on the 16-bit path, fit the workspace */
@@ -981,12 +998,13 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
     hipError_t e = hipSuccess;
     if (use16) {
       e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
-                                                   part_bytes, s)
+                                                   part_bytes, silu_pair, s)
           : mt < 256u ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
-                                                   part_bytes, s)
+                                                   part_bytes, silu_pair, s)
                       : launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, part,
-                                                   part_bytes, s);
+                                                   part_bytes, silu_pair, s);
     } else {
+      if (silu_pair) return hipErrorInvalidValue; /* the pair form needs the 16-bit path */
       for (uint32_t i = 0; i < count && e == hipSuccess; ++i)
         e = mt <= 32u    ? launch_tt<F, 32, 8, 256, 2>(*vs[i], mt, xt, yt[i], gt, bf16, part,
                                                        part_bytes, s)
@@ -1000,15 +1018,6 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
   return hipSuccess;
 }
 
-/* h = silu(h) * u elementwise (the gate/up epilogue as its own launch,
- * when both products were split over K). */
-template <int = 0>
-__global__ void __launch_bounds__(256) k_silu_mul(float *__restrict__ h,
-                                                  const float *__restrict__ u, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (size_t)gridDim.x * 256u)
-    h[i] = silu_mul(h[i], u[i]);
-}
-
 } // namespace paik
 
 using namespace paik;
@@ -1019,13 +1028,13 @@ using namespace paik;
 #define PAI_GEMM_ARGS                                                                         \
   const paik_qview_t *const *vs, float *const *ys, uint32_t count, uint32_t m, const float *x, \
       const float *gate, int bf16, void *x16, uint64_t x16_bytes, void *part,                  \
-      uint64_t part_bytes, void *stream
+      uint64_t part_bytes, int silu_pair, void *stream
 #ifdef PAI_GEMM_FMT
 extern "C" int PAI_GEMM_ENTRY(PAI_GEMM_ARGS) {
   return (int)launch_gemm<PAI_GEMM_FMT>(vs, ys, count, m, x, gate, bf16 != 0,
                                         static_cast<uint16_t *>(x16), (size_t)x16_bytes,
                                         static_cast<float *>(part), (size_t)part_bytes,
-                                        (hipStream_t)stream);
+                                        silu_pair != 0, (hipStream_t)stream);
 }
 #else
 extern "C" int paik_gemm_mfma_q4_0(PAI_GEMM_ARGS);
@@ -1035,24 +1044,27 @@ extern "C" int paik_gemm_mfma_q6_k(PAI_GEMM_ARGS);
 extern "C" int paik_gemm_mfma_multi(PAI_GEMM_ARGS) {
   if (count == 0u || count > (uint32_t)kGemmMats || (gate != nullptr && count != 1u))
     return (int)hipErrorInvalidValue;
+  if (silu_pair && (count != 2u || vs[0]->n != vs[1]->n || gate != nullptr))
+    return (int)hipErrorInvalidValue;
   for (uint32_t i = 1; i < count; ++i)
     if (vs[i]->type != vs[0]->type || vs[i]->k != vs[0]->k) return (int)hipErrorInvalidValue;
   switch (vs[0]->type) {
   case 8u: return paik_gemm_mfma_q8_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
-                                   part_bytes, stream);
+                                   part_bytes, silu_pair, stream);
   case 2u: return paik_gemm_mfma_q4_0(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
-                                   part_bytes, stream);
+                                   part_bytes, silu_pair, stream);
   case 12u: return paik_gemm_mfma_q4_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
-                                   part_bytes, stream);
+                                   part_bytes, silu_pair, stream);
   case 14u: return paik_gemm_mfma_q6_k(vs, ys, count, m, x, gate, bf16, x16, x16_bytes, part,
-                                   part_bytes, stream);
+                                   part_bytes, silu_pair, stream);
   default: return (int)hipErrorInvalidValue;
   }
 }
 extern "C" int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x, float *y,
                               const float *gate, int bf16, void *x16, uint64_t x16_bytes,
                               void *stream) {
-  return paik_gemm_mfma_multi(&v, &y, 1u, m, x, gate, bf16, x16, x16_bytes, nullptr, 0u, stream);
+  return paik_gemm_mfma_multi(&v, &y, 1u, m, x, gate, bf16, x16, x16_bytes, nullptr, 0u, 0,
+                              stream);
 }
 extern "C" uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m) {
   GemmArgs a;
@@ -1081,11 +1093,5 @@ extern "C" uint64_t paik_gemm_part_bytes(const paik_qview_t *const *vs, uint32_t
   }
   plan_grid(a, rwg, tt);
   return a.splits > 1u ? (uint64_t)a.splits * m * rows * 4u : 0u;
-}
-extern "C" int paik_silu_mul_inplace(float *h, const float *u, uint64_t n, void *stream) {
-  const uint64_t blocks = (n + 255u) / 256u;
-  k_silu_mul<><<<dim3((unsigned)(blocks < 4096u ? blocks : 4096u)), 256, 0, (hipStream_t)stream>>>(
-      h, u, (size_t)n);
-  return (int)hipGetLastError();
 }
 #endif
