@@ -545,6 +545,19 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
   }
   st = launch_mfma(w_gate, m, x, h, NULL, flags, s);
   if (st != PAI_OK) return st;
+  /* the up launch reads the 16-bit copy of x the gate launch just made,
+   * when that holds every token (one conversion instead of two) */
+  if (m <= PAI_X16_TOKENS && getenv("PAI_GEMM_NO_X16") == NULL) {
+    uint64_t wb = 0;
+    void *x16 = x16_workspace(w_gate, m, s, &wb);
+    if (x16 != NULL && wb >= ((m + 255u) & ~(uint64_t)255u) * w_gate->k * 2u) {
+      const paik_qview_t *vu = &w_up->view;
+      const int e = paik_gemm_mfma_multi(&vu, &h, 1u, (uint32_t)m, NULL, h,
+                                         (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, NULL, 0u,
+                                         0, s);
+      return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+    }
+  }
   return launch_mfma(w_up, m, x, h, h, flags, s);
 }
 

@@ -129,7 +129,9 @@ int paik_gemm_mfma(const paik_qview_t *v, uint32_t m, const float *x,
  * otherwise it zero-fills y and adds the parts with atomics. silu_pair:
  * vs = {gate, up} of one shape, and the second launch writes
  * ys[0] = silu(x W_gate^T) * (x W_up^T) (needs the parts: a split launch, a
- * large enough part workspace and the 16-bit path for all m tokens). */
+ * large enough part workspace and the 16-bit path for all m tokens).
+ * x == NULL: x16 already holds the 16-bit copy of all m tokens (written by
+ * an earlier call with the same x and bf16 flag); no conversion runs. */
 int paik_gemm_mfma_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                          uint32_t m, const float *x, const float *gate, int bf16, void *x16,
                          uint64_t x16_bytes, void *part, uint64_t part_bytes, int silu_pair,

@@ -920,12 +920,15 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
                              bool bf16, float *part, size_t part_bytes, bool silu_pair,
                              hipStream_t s) {
   const paik_qview_t &v = *vs[0];
-  const size_t n4 = (size_t)m * v.k / 4u;
-  const size_t blocks = (n4 + 255u) / 256u;
-  k_cvt_x<><<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
-      reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(x16), n4, bf16 ? 1 : 0);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  if (x != nullptr) { /* x == nullptr: x16 already holds these tokens */
+    const size_t n4 = (size_t)m * v.k / 4u;
+    const size_t blocks = (n4 + 255u) / 256u;
+    k_cvt_x<><<<dim3((unsigned)(blocks < 2048u ? blocks : 2048u)), 256, 0, s>>>(
+        reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(x16), n4, bf16 ? 1 : 0);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   GemmArgs a;
   memset(&a, 0, sizeof a);
   a.v = v;
@@ -985,9 +988,11 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
     const uint32_t fit = (uint32_t)((x16_bytes / ((size_t)v.k * 2u)) & ~(size_t)255u);
     if (fit < blk) blk = fit;
   }
+  /* x == nullptr: the 16-bit workspace already holds all m tokens */
+  if (x == nullptr && (!use16 || m > blk)) return hipErrorInvalidValue;
   for (uint32_t t0 = 0; t0 < m; t0 += blk) {
     const uint32_t mt = m - t0 < blk ? m - t0 : blk;
-    const float *xt = x + (size_t)t0 * v.k;
+    const float *xt = x != nullptr ? x + (size_t)t0 * v.k : nullptr;
     float *yt[kGemmMats];
     for (uint32_t i = 0; i < count; ++i) yt[i] = ys[i] + (size_t)t0 * vs[i]->n;
     const float *gt = gate != nullptr ? gate + (size_t)t0 * v.n : nullptr;
