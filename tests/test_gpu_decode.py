@@ -172,6 +172,34 @@ def test_projection_adds_to_residual(qtype, k, n):
     assert np.array_equal(by.download(n).view(np.uint32), (y1 + prod).view(np.uint32))
 
 
+def test_fused_projection_argument_errors():
+    """The fused projections reject misaligned pointers, mixed formats or
+    K, too many matrices and a K beyond the fused RMSNorm's limit before
+    any launch."""
+    say("[gpu] fused projection argument errors")
+    _, a = packed(pa.Q4_K, 64, 1024, 0xE01)
+    _, b = packed(pa.Q4_0, 64, 1024, 0xE02)
+    _, c = packed(pa.Q4_K, 64, 2048, 0xE03)
+    _, big = packed(pa.Q4_K, 8, 16640, 0xE04)
+    x, g, y = dev(np.ones(16640, np.float32)), dev(np.ones(16640, np.float32)), hm.DeviceBuffer(4 * 64)
+    hs = lambda *ms: ptr_array([m.handle for m in ms])
+    ys = lambda n: ptr_array([y.ptr] * n)
+    f = lib().pai_qgemv_rmsnorm_f32_async
+    assert f(hs(a), 1, x.ptr + 4, g.ptr, 0.0, ys(1), None) == -1        # x not 16-byte aligned
+    assert f(hs(a), 1, x.ptr, g.ptr + 4, 0.0, ys(1), None) == -1        # gamma not aligned
+    assert f(hs(a, b), 2, x.ptr, g.ptr, 0.0, ys(2), None) == -6         # formats differ
+    assert f(hs(a, c), 2, x.ptr, g.ptr, 0.0, ys(2), None) == -6         # K differs
+    assert f(hs(a, a, a, a), 4, x.ptr, g.ptr, 0.0, ys(4), None) == -1   # at most 3 matrices
+    assert f(hs(big), 1, x.ptr, g.ptr, 0.0, ys(1), None) == -3          # K above 16384
+    gu = lib().pai_qgemv_rmsnorm_gate_up_async
+    _, a2 = packed(pa.Q4_K, 32, 1024, 0xE05)
+    assert gu(a.handle, a2.handle, x.ptr, g.ptr, 0.0, y.ptr, None) == -6  # shapes differ
+    assert gu(a.handle, b.handle, x.ptr, g.ptr, 0.0, y.ptr, None) == -6   # formats differ
+    add = lib().pai_qgemv_add_f32_async
+    assert add(a.handle, x.ptr + 4, y.ptr, None) == -1
+    assert add(a.handle, x.ptr, y.ptr + 2, None) == -1
+
+
 @pytest.mark.parametrize("hq,hk,hd,r2", [(32, 8, 128, 64), (4, 2, 64, 16), (2, 1, 256, 128)])
 @pytest.mark.parametrize("pos", [0, 17, 63])
 def test_rope_kv_append(hq, hk, hd, r2, pos):
