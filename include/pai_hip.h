@@ -74,6 +74,21 @@ pai_status_t pai_hip_shutdown(void);
 /* Human-readable text of the last failure on this thread ("" if none). */
 const char *pai_hip_last_error(void);
 
+/* Launch-shape overrides for measurements and tests. All knobs start at 0,
+ * which is the shipped dispatch; nothing reads the environment. Not
+ * thread-safe against concurrent compute calls (set them before enqueuing).
+ * No counterpart in the reference. INVALID_ARG for an unknown knob or a
+ * negative value; out-of-range values are ignored by the dispatch. */
+#define PAI_TUNE_GEMM_SPLITS 1u        /* MFMA GEMM K parts, 1..64            */
+#define PAI_TUNE_GEMM_NO_X16 2u        /* 1: MFMA path without the 16-bit copy */
+#define PAI_TUNE_GEMM_ATOMIC_SPLITS 3u /* 1: multi-matrix parts via atomics   */
+#define PAI_TUNE_GEMV_WGS 4u           /* GEMV workgroups                     */
+#define PAI_TUNE_GEMV_ROWS 5u          /* GEMV rows per group: 1, 2 or 4      */
+#define PAI_TUNE_GEMV_NW 6u            /* one-token GEMV waves: 8 or 16       */
+#define PAI_TUNE_GEMV_NO_MX 7u         /* 1: no matrix-core GEMV for 2..8 tokens */
+#define PAI_TUNE_MFMA_MIN_M 8u         /* tokens from which the MFMA GEMM runs */
+pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value);
+
 /* Bytes occupied by `numel` elements of `type`; 0 when numel is not a
  * whole number of blocks or the type is not one of the four above.
  * Same semantics as pai_gguf_type_bytes (adapters/llama/gguf.c:562-597)
@@ -198,9 +213,19 @@ pai_status_t pai_qmat_upload_gguf(pai_qmat_t **out, const pai_gguf_dir_t *d,
  *    within rel-L2 1e-5.
  *  - Otherwise (the 16-bit MFMA path): blocks are dequantized in registers to fp16 (default) or
  *    bf16, x is rounded to the same type, and MFMA accumulates in f32.
- *    Tolerance: rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16). Each matrix keeps
- *    a device workspace for a 16-bit copy of up to 1024 tokens of x,
- *    allocated by the first such call made outside stream capture.
+ *    Tolerance: rel-L2 <= 2e-3 (fp16), <= 1.6e-2 (bf16). fp16 operands
+ *    need |x| < 65504 (larger values become inf); bf16 has the f32 range.
+ *    Each matrix keeps a device workspace for a 16-bit copy of up to 1024
+ *    tokens of x, allocated by the first such call made outside stream
+ *    capture. Workspaces only grow: a buffer replaced by a larger one stays
+ *    allocated until pai_qmat_free, because a HIP graph captured earlier
+ *    still refers to it. Destroy every graph that used a handle before
+ *    freeing the handle.
+ *    Repeatability: results repeat bit for bit, except for single-matrix
+ *    launches that split K into more than two parts (few row tiles, long
+ *    K: e.g. K = 14336 at 8 to 512 tokens), whose parts are added with f32
+ *    atomics in arrival order; those differ between calls in the last
+ *    bits, within the tolerance above.
  * Without PAI_QGEMM_DEVICE_PTRS, x and y are host pointers and the call
  * copies them; with it, they are device pointers. Synchronous.
  * Replaces pai_ref_gemm_f32 at scheduler/scheduler.c:340 for a weight
@@ -223,8 +248,11 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
  * kernels are enqueued. On the integer-dot path (see pai_qgemm_f32) the
  * matrices are multiplied in one launch per token group, which streams all
  * of their blocks and converts x once; results are bit-identical to
- * separate pai_qgemm_f32_async calls. On the 16-bit MFMA path each matrix
- * takes the MFMA path of pai_qgemm_f32_async.
+ * separate pai_qgemm_f32_async calls. On the 16-bit MFMA path the matrices
+ * share one launch, whose K split is chosen for all of them together and
+ * whose parts are summed in a fixed order: results are within the MFMA
+ * tolerance of separate calls, and bit-identical to them when neither
+ * splits K.
  * No counterpart in the reference, whose executor runs each projection as
  * its own pai_ref_gemm_f32 (scheduler/scheduler.c:340); this is the fused
  * form of those calls for weights that share an input value
@@ -256,8 +284,11 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate,
 
 /* out[N][K] = dequantized W in the native element order, computed on the
  * GPU from the device copy; bit-identical to pai_gguf_dequant
- * (adapters/llama/gguf.c:650-967) for every row. Host pointer unless
- * PAI_QGEMM_DEVICE_PTRS. Synchronous. */
+ * (adapters/llama/gguf.c:650-967) for every value, with one exception: a
+ * block whose f16 scale is a NaN gives a quiet NaN, where the reference
+ * keeps the scale's payload bits (gguf.c:620-621). Every other f16 scale
+ * pattern, subnormals and infinities included, converts identically. Host
+ * pointer unless PAI_QGEMM_DEVICE_PTRS. Synchronous. */
 pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags);
 
 /* ---------------------------------------------------------------------- */

@@ -23,6 +23,7 @@ SIGNATURES = {
     "pai_hip_init": (C.c_int32, []),
     "pai_hip_shutdown": (C.c_int32, []),
     "pai_hip_last_error": (C.c_char_p, []),
+    "pai_hip_set_tuning": (C.c_int32, [C.c_uint32, C.c_int32]),
     "pai_qtype_bytes": (C.c_uint64, [C.c_uint32, C.c_uint64]),
     "pai_qmat_upload": (C.c_int32, [C.POINTER(C.c_void_p), C.c_uint32, C.c_uint64,
                                     C.c_uint64, _vp, C.c_uint64]),

@@ -33,6 +33,14 @@ struct pai_qmat {
   /* the split parts of MFMA launches led by this handle (see part_workspace) */
   void *pw;
   uint64_t pw_bytes;
+  /* workspaces replaced by larger ones: a HIP graph captured earlier may
+   * still use them, so they are freed only with the handle */
+  struct pai_retired *retired;
+};
+
+struct pai_retired {
+  void *p;
+  struct pai_retired *next;
 };
 
 /* ---------------------------------------------------------------------- */
@@ -53,6 +61,30 @@ __attribute__((visibility("hidden"))) pai_status_t pai__fail(pai_status_t st, co
 #define fail pai__fail
 
 const char *pai_hip_last_error(void) { return t_err; }
+
+/* ---------------------------------------------------------------------- */
+/* Measurement knobs                                                        */
+/* ---------------------------------------------------------------------- */
+
+paik_tune_t paik_tune;
+
+pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value) {
+  int32_t *f;
+  switch (knob) {
+  case PAI_TUNE_GEMM_SPLITS: f = &paik_tune.gemm_splits; break;
+  case PAI_TUNE_GEMM_NO_X16: f = &paik_tune.gemm_no_x16; break;
+  case PAI_TUNE_GEMM_ATOMIC_SPLITS: f = &paik_tune.gemm_atomic_splits; break;
+  case PAI_TUNE_GEMV_WGS: f = &paik_tune.gemv_wgs; break;
+  case PAI_TUNE_GEMV_ROWS: f = &paik_tune.gemv_rows; break;
+  case PAI_TUNE_GEMV_NW: f = &paik_tune.gemv_nw; break;
+  case PAI_TUNE_GEMV_NO_MX: f = &paik_tune.gemv_no_mx; break;
+  case PAI_TUNE_MFMA_MIN_M: f = &paik_tune.mfma_min_m; break;
+  default: return fail(PAI_ERR_INVALID_ARG, "unknown tuning knob %u", knob);
+  }
+  if (value < 0) return fail(PAI_ERR_INVALID_ARG, "tuning value %d < 0", (int)value);
+  *f = value;
+  return PAI_OK;
+}
 
 /* hipError_t -> pai_status_t (sdk/include/pai/error.h codes). */
 static pai_status_t map_hip(hipError_t e, const char *what) {
@@ -93,6 +125,7 @@ static pai_status_t map_hip(hipError_t e, const char *what) {
 static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
 static int g_ready;
 static int g_device;
+
 
 /* Host-pointer staging (grow-only), guarded by g_stage_lock. */
 static pthread_mutex_t g_stage_lock = PTHREAD_MUTEX_INITIALIZER;
@@ -320,6 +353,12 @@ pai_status_t pai_qmat_free(pai_qmat_t *w) {
   if (w == NULL) return PAI_OK;
   if (w->x16 != NULL) (void)hipFree(w->x16);
   if (w->pw != NULL) (void)hipFree(w->pw);
+  while (w->retired != NULL) {
+    struct pai_retired *r = w->retired;
+    w->retired = r->next;
+    (void)hipFree(r->p);
+    free(r);
+  }
   hipError_t e = hipFree(w->dev);
   free(w);
   return e == hipSuccess ? PAI_OK : map_hip(e, "hipFree(weights)");
@@ -341,16 +380,10 @@ uint64_t pai_qmat_bytes(const pai_qmat_t *w) { return w != NULL ? w->packed_byte
 
 #define PAI_MFMA_MIN_M 8u
 /* Token count from which calls take the 16-bit MFMA GEMM; below it the
- * GEMV kernels (PAI_MFMA_MIN_M, or the PAI_MFMA_MIN_M environment value
- * for measurements). */
+ * GEMV kernels (PAI_MFMA_MIN_M, or the mfma_min_m tuning field). */
 static uint64_t mfma_min_m(void) {
-  static uint64_t v = 0;
-  if (v == 0) {
-    const char *e = getenv("PAI_MFMA_MIN_M");
-    const long r = e ? atol(e) : 0;
-    v = r >= 2 && r <= 4096 ? (uint64_t)r : PAI_MFMA_MIN_M;
-  }
-  return v;
+  const int32_t r = paik_tune.mfma_min_m;
+  return r >= 2 && r <= 4096 ? (uint64_t)r : PAI_MFMA_MIN_M;
 }
 
 /* Calls that take the GEMV kernels: under mfma_min_m() tokens, the
@@ -374,24 +407,29 @@ static pthread_mutex_t g_x16_lock = PTHREAD_MUTEX_INITIALIZER;
 
 /* A handle-owned device buffer of at least `want` bytes, grown outside
  * stream capture only (NULL with *bytes = 0, or the smaller buffer, during
- * capture). Caller holds g_x16_lock. */
-static void *grow_workspace(void **slot, uint64_t *slot_bytes, uint64_t want, hipStream_t s,
-                            uint64_t *bytes) {
+ * capture). The buffer it replaces is not freed: a graph captured earlier
+ * may still read and write it, so it joins the handle's retired list and is
+ * freed by pai_qmat_free. Buffers only grow, and the largest size is
+ * bounded (PAI_X16_TOKENS tokens), so the list stays short. Caller holds
+ * g_x16_lock. */
+static void *grow_workspace(pai_qmat_t *w, void **slot, uint64_t *slot_bytes, uint64_t want,
+                            hipStream_t s, uint64_t *bytes) {
   if (*slot == NULL || *slot_bytes < want) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
       void *p = NULL;
-      if (*slot != NULL) {
-        (void)hipStreamSynchronize(s); /* earlier calls on s may still read it */
-        (void)hipFree(*slot);
-        *slot = NULL;
-        *slot_bytes = 0;
-      }
-      if (hipMalloc(&p, want) == hipSuccess) {
+      struct pai_retired *r = *slot != NULL ? (struct pai_retired *)malloc(sizeof *r) : NULL;
+      if ((*slot == NULL || r != NULL) && hipMalloc(&p, want) == hipSuccess) {
+        if (r != NULL) {
+          r->p = *slot;
+          r->next = w->retired;
+          w->retired = r;
+        }
         *slot = p;
         *slot_bytes = want;
       } else {
-        (void)hipGetLastError(); /* no workspace: the caller takes its other path */
+        free(r);
+        (void)hipGetLastError(); /* keep the old buffer: the caller fits its work to it */
       }
     }
   }
@@ -403,7 +441,7 @@ static void *x16_workspace(const pai_qmat_t *cw, uint64_t m, hipStream_t s, uint
   pai_qmat_t *w = (pai_qmat_t *)cw;
   const uint64_t tok = ((m < PAI_X16_TOKENS ? m : PAI_X16_TOKENS) + 255u) & ~(uint64_t)255u;
   pthread_mutex_lock(&g_x16_lock);
-  void *p = grow_workspace(&w->x16, &w->x16_bytes, tok * w->k * 2u, s, bytes);
+  void *p = grow_workspace(w, &w->x16, &w->x16_bytes, tok * w->k * 2u, s, bytes);
   pthread_mutex_unlock(&g_x16_lock);
   return p;
 }
@@ -420,11 +458,11 @@ static void *part_workspace(const pai_qmat_t *cw, const paik_qview_t *const *vs,
                             uint64_t m, hipStream_t s, uint64_t *bytes) {
   pai_qmat_t *w = (pai_qmat_t *)cw;
   *bytes = 0;
-  if (count < 2u || getenv("PAI_GEMM_ATOMIC_SPLITS") != NULL) return NULL;
+  if (count < 2u || paik_tune.gemm_atomic_splits != 0) return NULL;
   const uint64_t want = paik_gemm_part_bytes(vs, count, (uint32_t)m);
   if (want == 0u) return NULL;
   pthread_mutex_lock(&g_x16_lock);
-  void *p = grow_workspace(&w->pw, &w->pw_bytes, want, s, bytes);
+  void *p = grow_workspace(w, &w->pw, &w->pw_bytes, want, s, bytes);
   pthread_mutex_unlock(&g_x16_lock);
   return p;
 }
@@ -435,7 +473,7 @@ static pai_status_t launch_mfma_multi(const pai_qmat_t *const *ws, uint32_t coun
                                       const float *x, float *const *ys, const float *gate,
                                       uint32_t flags, hipStream_t s) {
   uint64_t wb = 0, pb = 0;
-  void *x16 = getenv("PAI_GEMM_NO_X16") ? NULL : x16_workspace(ws[0], m, s, &wb);
+  void *x16 = paik_tune.gemm_no_x16 != 0 ? NULL : x16_workspace(ws[0], m, s, &wb);
   const paik_qview_t *vs[4];
   for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
   void *part = gate != NULL ? NULL : part_workspace(ws[0], vs, count, m, s, &pb);
@@ -528,7 +566,7 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
    * Otherwise (or without the workspaces, inside a capture) the gate
    * product lands in h and the up product's epilogue forms silu(gate) * up
    * in place (whole sums, no split). */
-  if (m <= PAI_X16_TOKENS && getenv("PAI_GEMM_NO_X16") == NULL &&
+  if (m <= PAI_X16_TOKENS && paik_tune.gemm_no_x16 == 0 &&
       paik_gemm_x16_splits(&w_up->view, (uint32_t)m) > 1u) {
     uint64_t wb = 0, pb = 0;
     void *x16 = x16_workspace(w_gate, m, s, &wb);
@@ -547,7 +585,7 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
   if (st != PAI_OK) return st;
   /* the up launch reads the 16-bit copy of x the gate launch just made,
    * when that holds every token (one conversion instead of two) */
-  if (m <= PAI_X16_TOKENS && getenv("PAI_GEMM_NO_X16") == NULL) {
+  if (m <= PAI_X16_TOKENS && paik_tune.gemm_no_x16 == 0) {
     uint64_t wb = 0;
     void *x16 = x16_workspace(w_gate, m, s, &wb);
     if (x16 != NULL && wb >= ((m + 255u) & ~(uint64_t)255u) * w_gate->k * 2u) {

@@ -48,6 +48,22 @@ typedef struct paik_qview {
   uint32_t pad_;
 } paik_qview_t;
 
+/* Launch-shape overrides for measurements, set only through
+ * pai_hip_set_tuning (never from the environment). Zero everywhere is the
+ * shipped dispatch; each field is read where the corresponding choice is
+ * made. Defined in pai_hip.c. */
+typedef struct paik_tune {
+  int32_t gemm_splits;        /* MFMA GEMM K parts (1..64; 0: planned)           */
+  int32_t gemm_no_x16;        /* 1: MFMA path without the 16-bit workspace        */
+  int32_t gemm_atomic_splits; /* 1: multi-matrix split parts added with atomics   */
+  int32_t gemv_wgs;           /* GEMV workgroups (1..65535; 0: planned)           */
+  int32_t gemv_rows;          /* GEMV rows per group (1, 2, 4; 0: planned)        */
+  int32_t gemv_nw;            /* one-token GEMV waves per workgroup (8, 16; 0)    */
+  int32_t gemv_no_mx;         /* 1: 2..8-token calls stay on the integer-dot GEMV */
+  int32_t mfma_min_m;         /* tokens from which calls take the MFMA GEMM (0: 8) */
+} paik_tune_t;
+extern paik_tune_t paik_tune;
+
 /* Plane offsets of a matrix inside one device allocation (256-byte
  * aligned planes). Returns the total bytes to allocate, 0 on bad input. */
 uint64_t paik_plan_layout(uint32_t type, uint64_t n, uint64_t k,

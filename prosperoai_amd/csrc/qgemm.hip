@@ -807,10 +807,8 @@ static void plan_grid(GemmArgs &a, uint32_t rwg, uint32_t tt) {
    * the chip (one or two parts stay exact and repeatable). */
   if (splits > 2u)
     while (tiles * splits * 2u <= 256u && nsteps / (splits * 2u) >= 4u) splits *= 2u;
-  if (const char *e = getenv("PAI_GEMM_SPLITS")) {
-    const int r = atoi(e);
-    if (r >= 1 && r <= 64) splits = (uint32_t)r;
-  }
+  if (paik_tune.gemm_splits >= 1 && paik_tune.gemm_splits <= 64)
+    splits = (uint32_t)paik_tune.gemm_splits;
   if (a.gate != nullptr) splits = 1u; /* the epilogue needs whole sums */
   a.steps_per_split = (nsteps + splits - 1u) / splits;
   a.steps_per_split = (a.steps_per_split + 3u) & ~3u; /* the loop runs steps in fours */

@@ -462,14 +462,11 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 /* Workgroups: one per CU (256), fewer when that would leave waves with
  * under two rows (a one-row group re-reads the activation planes for a
  * single row). Rows per group U: 4 when waves get four or more rows, else
- * 2 (U*MT <= 8). PAI_GEMV_WGS / PAI_GEMV_ROWS override both (tuning). */
+ * 2 (U*MT <= 8). The gemv_wgs / gemv_rows tuning fields override both. */
 static uint32_t pick_grid(uint32_t n, uint32_t count) {
   uint32_t g = (n + 2u * kWaves - 1u) / (2u * kWaves);
   if (g > 256u) g = 256u;
-  if (const char *e = getenv("PAI_GEMV_WGS")) {
-    const int r = atoi(e);
-    if (r >= 1 && r <= 65535) g = (uint32_t)r;
-  }
+  if (paik_tune.gemv_wgs >= 1 && paik_tune.gemv_wgs <= 65535) g = (uint32_t)paik_tune.gemv_wgs;
   const uint32_t need = (n + kWaves - 1u) / kWaves; /* at least one row per wave */
   if (need < g) g = need;
   const uint32_t least = (count + kWaves - 1u) / kWaves; /* a wave per matrix */
@@ -480,10 +477,8 @@ template <int MT>
 static int pick_rows(uint32_t n, uint32_t grid) {
   const uint32_t rw = (n + grid * kWaves - 1u) / (grid * kWaves);
   int u = (rw >= 4u && 4 * MT <= 8) ? 4 : (2 * MT <= 8 ? 2 : 1);
-  if (const char *e = getenv("PAI_GEMV_ROWS")) {
-    const int r = atoi(e);
-    if ((r == 1 || r == 2 || r == 4) && r * MT <= 8) u = r;
-  }
+  const int r = paik_tune.gemv_rows;
+  if ((r == 1 || r == 2 || r == 4) && r * MT <= 8) u = r;
   return u;
 }
 
@@ -512,10 +507,10 @@ static uint32_t slice_cap(uint32_t mt, int nw = kWaves, int xi = kXIt) {
 /* One-token launches of up to 4096 rows (two rows per wave on 256
  * workgroups of 8 waves) run on that grid instead of half as many 16-wave
  * workgroups, so every CU shares the dot-product work, when a row still
- * fits one column slice of the smaller plane builder (PAI_GEMV_NW=16 / 8
- * forces either). */
+ * fits one column slice of the smaller plane builder (the gemv_nw tuning
+ * field, 16 or 8, forces either). */
 static bool small_wg(uint32_t rows, uint32_t k, int xi = kXIt) {
-  static const int nw = getenv("PAI_GEMV_NW") ? atoi(getenv("PAI_GEMV_NW")) : 0;
+  const int nw = paik_tune.gemv_nw;
   if ((k >> 5) > slice_cap(1u, kWavesSmall, xi)) return false; /* rows stay one slice */
   if (nw == 16) return false;
   if (nw == 8) return true;
@@ -616,10 +611,10 @@ static hipError_t gemv_one(const paik_qview_t *const *vs, float *const *ys, uint
  * where it takes K: its weight operands are shared by all tokens of a
  * launch, while this kernel's integer dots are paid per token. One token
  * stays here, where the dots are cheaper than the matrix-core operand
- * layout's scattered loads. PAI_GEMV_NO_MX=1 keeps every call here. */
+ * layout's scattered loads. The gemv_no_mx tuning field keeps every call
+ * here. */
 static bool use_mx(uint32_t k, uint32_t m) {
-  static const bool off = getenv("PAI_GEMV_NO_MX") != nullptr;
-  return !off && m >= 2u && paik_gemv_mx_tokens(k, m) != 0u;
+  return paik_tune.gemv_no_mx == 0 && m >= 2u && paik_gemv_mx_tokens(k, m) != 0u;
 }
 
 template <class F>

@@ -51,6 +51,33 @@ def init() -> None:
     check(lib().pai_hip_init(), "pai_hip_init")
 
 
+# pai_hip_set_tuning knobs (include/pai_hip.h)
+TUNE = {"gemm_splits": 1, "gemm_no_x16": 2, "gemm_atomic_splits": 3, "gemv_wgs": 4,
+        "gemv_rows": 5, "gemv_nw": 6, "gemv_no_mx": 7, "mfma_min_m": 8}
+
+
+def set_tuning(name: str, value: int) -> None:
+    """Launch-shape override for measurements and tests (0 = shipped dispatch)."""
+    check(lib().pai_hip_set_tuning(TUNE[name], int(value)), "pai_hip_set_tuning")
+
+
+class tuning:
+    """Context manager: knobs set on entry, back to 0 on exit."""
+
+    def __init__(self, **knobs):
+        self.knobs = knobs
+
+    def __enter__(self):
+        for k, v in self.knobs.items():
+            set_tuning(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k in self.knobs:
+            set_tuning(k, 0)
+        return False
+
+
 def descriptors() -> list[HipDescriptor]:
     count = C.c_uint32(0)
     ptr = lib().pai_hip_op_descriptors(C.byref(count))

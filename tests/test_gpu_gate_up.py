@@ -102,11 +102,11 @@ def test_gemv_gate_up_longest_rows():
 
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
 @pytest.mark.parametrize("m", [8, 33, 300])
-def test_mfma_gate_up_unsplit_matches_composition(monkeypatch, qtype, m):
-    monkeypatch.setenv("PAI_GEMM_SPLITS", "1")
+def test_mfma_gate_up_unsplit_matches_composition(qtype, m):
     n, k = 320, 1024
     say(f"[gpu] gate_up mfma unsplit type={qtype} m={m}")
-    h, g, u, *_ = run(qtype, n, k, m, 5000 + 10 * qtype + m)
+    with pa.tuning(gemm_splits=1):
+        h, g, u, *_ = run(qtype, n, k, m, 5000 + 10 * qtype + m)
     assert max_ulps(h, ob.silu_mul(g, u)) <= 4
 
 

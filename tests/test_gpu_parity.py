@@ -249,21 +249,21 @@ def test_prefill_shape_down_q6k_m512():
 
 
 @pytest.mark.parametrize("splits", [2, 3, 7])
-def test_mfma_forced_split_k_ragged(monkeypatch, splits):
+def test_mfma_forced_split_k_ragged(splits):
     """K split into uneven ranges, last step with a single chunk."""
-    monkeypatch.setenv("PAI_GEMM_SPLITS", str(splits))
     for qtype, m in ((2, 70), (8, 33)):
         n, k = 300, 32 * 37
         say(f"[gpu] gemm MFMA split={splits} type={qtype} m={m}")
         blocks = weights(qtype, n, k, 90 + splits + qtype)
         x = pa.normal_f32(91 + splits, m * k).reshape(m, k)
-        y = pa.QMat(qtype, n, k, blocks).gemm(x)
+        with pa.tuning(gemm_splits=splits):
+            y = pa.QMat(qtype, n, k, blocks).gemm(x)
         assert rel_l2(y, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
 
 
 @pytest.mark.parametrize("qtype", [2, 8, 12, 14])
 @pytest.mark.parametrize("m", [40, 300])
-def test_mfma_16bit_copy_matches_register_staging(monkeypatch, qtype, m):
+def test_mfma_16bit_copy_matches_register_staging(qtype, m):
     """The activations reach LDS either from the matrix's 16-bit workspace
     (DMA) or through registers; both round x the same way and accumulate in
     the same order, so the outputs are identical."""
@@ -273,8 +273,8 @@ def test_mfma_16bit_copy_matches_register_staging(monkeypatch, qtype, m):
     x = pa.normal_f32(121 + m, m * k).reshape(m, k)
     qm = pa.QMat(qtype, n, k, blocks)
     y16 = qm.gemm(x)
-    monkeypatch.setenv("PAI_GEMM_NO_X16", "1")
-    yreg = qm.gemm(x)
+    with pa.tuning(gemm_no_x16=1):
+        yreg = qm.gemm(x)
     assert np.array_equal(y16, yreg)
     assert rel_l2(y16, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
 
