@@ -221,11 +221,12 @@ pai_status_t pai_qmat_upload_gguf(pai_qmat_t **out, const pai_gguf_dir_t *d,
  *    allocated until pai_qmat_free, because a HIP graph captured earlier
  *    still refers to it. Destroy every graph that used a handle before
  *    freeing the handle.
- *    Repeatability: results repeat bit for bit, except for single-matrix
- *    launches that split K into more than two parts (few row tiles, long
- *    K: e.g. K = 14336 at 8 to 512 tokens), whose parts are added with f32
- *    atomics in arrival order; those differ between calls in the last
- *    bits, within the tolerance above.
+ *    Repeatability: results repeat bit for bit, except where a
+ *    single-matrix launch whose tiles do not fill the chip splits K into
+ *    more than two parts (e.g. 4096 rows at 40 or 512 tokens, 4096 x 14336
+ *    at 8 to 512 tokens): its parts are added with f32 atomics in arrival
+ *    order, and the sums differ between calls in the last bits, within the
+ *    tolerance above. Multi-matrix calls sum their parts in a fixed order.
  * Without PAI_QGEMM_DEVICE_PTRS, x and y are host pointers and the call
  * copies them; with it, they are device pointers. Synchronous.
  * Replaces pai_ref_gemm_f32 at scheduler/scheduler.c:340 for a weight
@@ -239,6 +240,25 @@ pai_status_t pai_qgemm_f32(const pai_qmat_t *w, uint64_t m, const float *x,
 pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m,
                                  const float *x, float *y, uint32_t flags,
                                  void *stream);
+
+/* pai_qgemm_f32_async that allocates nothing: no hipMalloc, hipFree or
+ * other allocating call, on any path. On the 16-bit MFMA path the 16-bit
+ * copy of x lives in a 16 MiB device array of the library (one per GPU,
+ * held until the process ends) instead of the handle's workspace, in token
+ * blocks that fit it; the GEMV paths need no scratch. Same arguments,
+ * errors and numerics as pai_qgemm_f32_async; results are bit-identical to
+ * it wherever that call's launches repeat bit for bit and both run the
+ * tokens as one block (up to 16 MiB / (2 K) tokens, rounded down to a
+ * multiple of 256, and at most 1024). PAI_ERR_UNSUPPORTED when the MFMA
+ * path would need K > 32768 (256 tokens of 16-bit activations must fit).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race; serialise them on one stream.
+ * No counterpart in the reference. It exists for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, and
+ * harnesses that forbid device allocation. */
+pai_status_t pai_qgemm_f32_noalloc_async(const pai_qmat_t *w, uint64_t m,
+                                         const float *x, float *y,
+                                         uint32_t flags, void *stream);
 
 /* Fused projections: y_i[m][N_i] = x[m][K] * W_i^T for `count` (1..4)
  * matrices that share the activations (the q/k/v or gate/up projections

@@ -35,6 +35,7 @@ SIGNATURES = {
     "pai_qmat_bytes": (C.c_uint64, [_vp]),
     "pai_qgemm_f32": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32]),
     "pai_qgemm_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32, _vp]),
+    "pai_qgemm_f32_noalloc_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, C.c_uint32, _vp]),
     "pai_qgemm_f32_multi_async": (C.c_int32, [C.POINTER(C.c_void_p), C.c_uint32, C.c_uint64, _vp,
                                               C.POINTER(C.c_void_p), C.c_uint32, _vp]),
     "pai_qgemm_f32_gate_up_async": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp, C.c_uint32,

@@ -126,6 +126,12 @@ static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
 static int g_ready;
 static int g_device;
 
+/* Device address of each device's copy of the no-allocation scratch array
+ * (qscratch.hip), taken once per device with that device current: at
+ * pai_hip_init for the init device, else at that device's first
+ * no-allocation call. Guarded by g_lock. */
+#define PAI_MAX_DEVICES 64
+static void *g_scratch[PAI_MAX_DEVICES];
 
 /* Host-pointer staging (grow-only), guarded by g_stage_lock. */
 static pthread_mutex_t g_stage_lock = PTHREAD_MUTEX_INITIALIZER;
@@ -161,10 +167,44 @@ pai_status_t pai_hip_init(void) {
     return fail(PAI_ERR_INIT, "device %d is %s; kernels are built for gfx950", dev,
                 prop.gcnArchName);
   }
+  if (dev >= 0 && dev < PAI_MAX_DEVICES && g_scratch[dev] == NULL) {
+    const int se = paik_scratch_address(&g_scratch[dev]);
+    if (se != 0) {
+      pthread_mutex_unlock(&g_lock);
+      return map_hip((hipError_t)se, "hipGetSymbolAddress(scratch)");
+    }
+  }
   g_device = dev;
   g_ready = 1;
   pthread_mutex_unlock(&g_lock);
   return PAI_OK;
+}
+
+/* The current device's scratch address (NULL with the status on failure). */
+static void *scratch_here(pai_status_t *st) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *st = map_hip(e, "hipGetDevice");
+    return NULL;
+  }
+  if (dev < 0 || dev >= PAI_MAX_DEVICES) {
+    *st = fail(PAI_ERR_UNSUPPORTED, "device %d above %d", dev, PAI_MAX_DEVICES - 1);
+    return NULL;
+  }
+  pthread_mutex_lock(&g_lock);
+  if (g_scratch[dev] == NULL) {
+    const int se = paik_scratch_address(&g_scratch[dev]);
+    if (se != 0) {
+      pthread_mutex_unlock(&g_lock);
+      *st = map_hip((hipError_t)se, "hipGetSymbolAddress(scratch)");
+      return NULL;
+    }
+  }
+  void *p = g_scratch[dev];
+  pthread_mutex_unlock(&g_lock);
+  *st = PAI_OK;
+  return p;
 }
 
 pai_status_t pai_hip_shutdown(void) {
@@ -510,6 +550,39 @@ pai_status_t pai_qgemm_f32_async(const pai_qmat_t *w, uint64_t m, const float *x
   if (((uintptr_t)x & 15u) != 0u || ((uintptr_t)y & 3u) != 0u)
     return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned, y 4-byte aligned");
   return launch(w, m, x, y, flags, (hipStream_t)stream);
+}
+
+/* pai_qgemm_f32_async without allocations: the 16-bit MFMA path takes its
+ * copy of x from the current device's scratch array (PAIK_SCRATCH_BYTES,
+ * shared by every call on that device) in token blocks that fit it, in
+ * place of the handle's workspace; single-matrix launches split over K
+ * zero-fill y with a kernel and add their parts with atomics, as in
+ * pai_qgemm_f32_async. The GEMV paths use no scratch. Nothing here
+ * allocates or frees device or host memory. */
+pai_status_t pai_qgemm_f32_noalloc_async(const pai_qmat_t *w, uint64_t m, const float *x,
+                                         float *y, uint32_t flags, void *stream) {
+  pai_status_t st = check_call(w, m, x, y);
+  if (st != PAI_OK) return st;
+  if (((uintptr_t)x & 15u) != 0u || ((uintptr_t)y & 3u) != 0u)
+    return fail(PAI_ERR_INVALID_ARG, "x must be 16-byte aligned, y 4-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (gemv_call(w, m, flags)) {
+    const int e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
+    return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
+  }
+  /* the smallest token block of the 16-bit path is 256 tokens */
+  if (w->k * 2u * 256u > (uint64_t)PAIK_SCRATCH_BYTES)
+    return fail(PAI_ERR_UNSUPPORTED,
+                "K=%llu above %u: the no-allocation scratch (%u bytes) holds 256 tokens of "
+                "16-bit activations up to that K",
+                (unsigned long long)w->k, PAIK_SCRATCH_BYTES / 512u, PAIK_SCRATCH_BYTES);
+  void *scratch = scratch_here(&st);
+  if (scratch == NULL) return st;
+  const paik_qview_t *v = &w->view;
+  const int e = paik_gemm_mfma_multi(&v, &y, 1u, (uint32_t)m, x, NULL,
+                                     (flags & PAI_QGEMM_MFMA_BF16) != 0u, scratch,
+                                     PAIK_SCRATCH_BYTES, NULL, 0u, 0, s);
+  return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
 }
 
 #define PAI_MULTI_MAX 4u

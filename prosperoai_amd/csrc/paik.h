@@ -70,6 +70,12 @@ uint64_t paik_plan_layout(uint32_t type, uint64_t n, uint64_t k,
                           uint64_t *off_q, uint64_t *off_aux,
                           uint64_t *off_meta, uint64_t *off_d);
 
+/* The per-device scratch array of the no-allocation entry point
+ * (qscratch.hip): its size, and its device address on the current device
+ * (hipError_t as int; call with that device current). */
+#define PAIK_SCRATCH_BYTES (16u << 20)
+int paik_scratch_address(void **ptr);
+
 /* Launchers (HIP side). All return hipError_t as int; 0 on success. The
  * stream is a hipStream_t. Shapes are validated by the caller. */
 int paik_repack(const paik_qview_t *v, const uint8_t *native, void *stream);
