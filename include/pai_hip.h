@@ -87,6 +87,7 @@ const char *pai_hip_last_error(void);
 #define PAI_TUNE_GEMV_NW 6u            /* one-token GEMV waves: 8 or 16       */
 #define PAI_TUNE_GEMV_NO_MX 7u         /* 1: no matrix-core GEMV for 2..8 tokens */
 #define PAI_TUNE_MFMA_MIN_M 8u         /* tokens from which the MFMA GEMM runs */
+#define PAI_TUNE_GEMM_TILE 9u          /* 16-bit GEMM token tile: 1, 2, 3 = 32, 128, 256 */
 pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value);
 
 /* Bytes occupied by `numel` elements of `type`; 0 when numel is not a

@@ -79,6 +79,7 @@ pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value) {
   case PAI_TUNE_GEMV_NW: f = &paik_tune.gemv_nw; break;
   case PAI_TUNE_GEMV_NO_MX: f = &paik_tune.gemv_no_mx; break;
   case PAI_TUNE_MFMA_MIN_M: f = &paik_tune.mfma_min_m; break;
+  case PAI_TUNE_GEMM_TILE: f = &paik_tune.gemm_tile; break;
   default: return fail(PAI_ERR_INVALID_ARG, "unknown tuning knob %u", knob);
   }
   if (value < 0) return fail(PAI_ERR_INVALID_ARG, "tuning value %d < 0", (int)value);

@@ -61,6 +61,7 @@ typedef struct paik_tune {
   int32_t gemv_nw;            /* one-token GEMV waves per workgroup (8, 16; 0)    */
   int32_t gemv_no_mx;         /* 1: 2..8-token calls stay on the integer-dot GEMV */
   int32_t mfma_min_m;         /* tokens from which calls take the MFMA GEMM (0: 8) */
+  int32_t gemm_tile;          /* 16-bit GEMM tile: 1 = 32 tokens, 2 = 128, 3 = 256 (0: by M) */
 } paik_tune_t;
 extern paik_tune_t paik_tune;
 

@@ -912,11 +912,461 @@ static hipError_t launch_tt(const paik_qview_t &v, uint32_t m, const float *x, f
   return launch_reduce(part, &y, &n, 1u, m, a.splits, s);
 }
 
+
+/* ======================================================================
+ * Prefill GEMM with the weights shared through LDS (k_gemm_lds, 256 tokens
+ * and more per call).
+ *
+ * Workgroup: 8 waves (two per SIMD), 128 weight rows x 256 tokens. Each
+ * 64-column stage, every thread dequantizes 16 weights (one row, one
+ * quarter of the stage) once into the 16-bit weight tile, and the
+ * activation tile (256 tokens x 64 columns of the 16-bit copy) moves into
+ * LDS by DMA. Wave (wr, wt) = (wave % 2, wave / 2) then multiplies tokens
+ * 64 wt .. 64 wt + 63 by rows 64 wr .. 64 wr + 63: 2 x 2 fragments of
+ * v_mfma_f32_32x32x16 with the activations as A (32 tokens x 16 columns)
+ * and the weights as B (16 columns x 32 rows), both read from LDS. A lane's
+ * accumulator then holds one weight row for 16 tokens, so each store
+ * instruction writes 2 x 128 contiguous bytes of y and no transpose is
+ * needed.
+ *
+ * Why this shape: on gfx950 an MFMA loop that reads one 1 KiB LDS operand
+ * per 32x32x16 MFMA reaches 0.82 of the matrix peak with two waves per
+ * SIMD and 0.53-0.59 with one (probe), and dequantizing each weight once
+ * per 256 tokens keeps the dequantization near 1.5 VALU operations per
+ * MFMA. LDS: the weight tile double-buffered (2 x 16 KiB), the activation
+ * tile in four buffers (4 x 32 KiB), 160 KiB in all; with the buffer
+ * index of every stage known at compile time (the loop runs stages in
+ * fours), each operand read is one instruction with an immediate offset.
+ *
+ * Pipeline per stage s: DMA of activations s+2, weight loads of stage s+4
+ * (a ring of 4 register slots), the 16 MFMAs of stage s, dequantization of
+ * stage s+1 into the other weight tile, then one barrier. The waits count
+ * loads exactly (every wave issues the same sequence).
+ * ==================================================================== */
+namespace lg {
+constexpr int BM = 128;                  /* weight rows per workgroup */
+constexpr int BN = 256;                  /* tokens per workgroup */
+constexpr int KS = 64;                   /* columns per stage */
+constexpr int NW = 8;                    /* waves */
+constexpr int NT = 64 * NW;
+constexpr int kWTile = BM * KS * 2;      /* 16 KiB */
+constexpr int kXTile = BN * KS * 2;      /* 32 KiB */
+constexpr int kXDma = kXTile / 1024 / NW; /* DMA instructions per wave per stage */
+constexpr int kRing = 4;                 /* weight-load stages in flight */
+constexpr int kXBufs = 4;                /* activation tiles (stage s in buffer s % 4) */
+constexpr int kLds = 2 * kWTile + kXBufs * kXTile;
+static_assert(kLds <= 160 * 1024, "LDS");
+} // namespace lg
+
+/* Byte offset of 16-byte segment `seg` (columns 8 seg .. 8 seg + 7 of the
+ * stage) of tile row `row`. Two rows share a 256-byte line, whose 16 slots
+ * are permuted per line: the 16 rows a quarter-wave reads (one segment)
+ * land in 16 distinct slots, i.e. on every LDS bank once, and any 8
+ * consecutive rows in distinct slots modulo 128 bytes. */
+__device__ __forceinline__ uint32_t lg_off(uint32_t row, uint32_t seg) {
+  const uint32_t line = row >> 1;
+  return line * 256u + (((((seg ^ line) & 7u) << 1) | (row & 1u)) << 4);
+}
+
+/* Weight loads of k_gemm_lds, written as asm so that the compiler's wait
+ * insertion, which cannot count the activation DMA (also asm), leaves them
+ * alone: the kernel waits for them itself (qq_wait), with exact counts. */
+__device__ __forceinline__ u32x2 ql8(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  u32x2 v;
+  __asm__ volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+  return v;
+}
+__device__ __forceinline__ u32x4 ql16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  u32x4 v;
+  __asm__ volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+  return v;
+}
+__device__ __forceinline__ uint32_t ql4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+  return v;
+}
+__device__ __forceinline__ uint32_t ql2(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  uint32_t v;
+  __asm__ volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(r));
+  return v;
+}
+
+/* 16 columns of one row (nibble words 2h and 2h+1 of chunk c): the raw
+ * bytes as loaded (kLoads requests), a wait for them that also orders
+ * their uses after it (wait<N>: vmcnt N, the registers as operands), and
+ * their 16-bit values as two 8-column segments (value = s (1024 + q) + b
+ * as in Ops; zeros when !ok). */
+template <class F>
+struct QQ;
+template <>
+struct QQ<Q4_0> {
+  static constexpr int kLoads = 2;
+  struct Raw { u32x2 q; uint32_t d; };
+  __device__ static Raw get(const QRes &r, uint32_t row, uint32_t c, uint32_t h) {
+    Raw w;
+    w.q = ql8(r.q, row * r.q_stride + 16u * c + 8u * h);
+    w.d = ql2(r.d, (row * r.nb + c) * 2u);
+    return w;
+  }
+  template <int N>
+  __device__ static void wait(Raw &w) {
+    __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(w.q), "+v"(w.d) : "i"(N));
+  }
+  template <bool BF, int HI>
+  __device__ static void vals(const Raw &w, uint32_t, uint32_t, bool ok, uint4 &o0, uint4 &o1) {
+    const float d = ok ? h2f((uint16_t)w.d) : 0.0f, b = -1032.0f * d;
+    const uint32_t u0 = w.q[0] ^ 0x88888888u, u1 = w.q[1] ^ 0x88888888u;
+    o0 = word_op<BF>(u0 & 0x0F0F0F0Fu, (u0 >> 4) & 0x0F0F0F0Fu, d, b);
+    o1 = word_op<BF>(u1 & 0x0F0F0F0Fu, (u1 >> 4) & 0x0F0F0F0Fu, d, b);
+  }
+};
+template <>
+struct QQ<Q8_0> {
+  static constexpr int kLoads = 3;
+  struct Raw { u32x2 lo, hi; uint32_t d; };
+  __device__ static Raw get(const QRes &r, uint32_t row, uint32_t c, uint32_t h) {
+    const uint32_t o = row * r.q_stride + 32u * c + 8u * h;
+    Raw w;
+    w.lo = ql8(r.q, o);
+    w.hi = ql8(r.q, o + 16u);
+    w.d = ql2(r.d, (row * r.nb + c) * 2u);
+    return w;
+  }
+  template <int N>
+  __device__ static void wait(Raw &w) {
+    __asm__ volatile("s_waitcnt vmcnt(%3)" : "+v"(w.lo), "+v"(w.hi), "+v"(w.d) : "i"(N));
+  }
+  template <bool BF>
+  __device__ static uint4 word(uint32_t lo, uint32_t hi, float d, float b) {
+    const uint32_t l = lo ^ 0x88888888u, h = hi ^ 0x88888888u; /* byte = code + 128 */
+    return word_op<BF>(bfi(0xF0F0F0F0u, h << 4, l), bfi(0xF0F0F0F0u, h, l >> 4), d, b);
+  }
+  template <bool BF, int HI>
+  __device__ static void vals(const Raw &w, uint32_t, uint32_t, bool ok, uint4 &o0, uint4 &o1) {
+    const float d = ok ? h2f((uint16_t)w.d) : 0.0f, b = -1152.0f * d;
+    o0 = word<BF>(w.lo[0], w.hi[0], d, b);
+    o1 = word<BF>(w.lo[1], w.hi[1], d, b);
+  }
+};
+template <>
+struct QQ<Q4_K> {
+  static constexpr int kLoads = 2;
+  struct Raw { u32x2 q; u32x4 m; };
+  __device__ static Raw get(const QRes &r, uint32_t row, uint32_t c, uint32_t h) {
+    Raw w;
+    w.q = ql8(r.q, row * r.q_stride + 16u * c + 8u * h);
+    w.m = ql16(r.meta, (row * r.nb + (c >> 3)) * 16u);
+    return w;
+  }
+  template <int N>
+  __device__ static void wait(Raw &w) {
+    __asm__ volatile("s_waitcnt vmcnt(%2)" : "+v"(w.q), "+v"(w.m) : "i"(N));
+  }
+  /* HI: the chunk lies in sub-blocks 4..7 of its super-block */
+  template <bool BF, int HI>
+  __device__ static void vals(const Raw &w, uint32_t c, uint32_t, bool ok, uint4 &o0, uint4 &o1) {
+    const int i = (int)(c & 3u);
+    const uint32_t b0 = byte_of(w.m[1], i), b1 = byte_of(w.m[2], i);
+    uint32_t sc, mn;
+    if constexpr (HI != 0) {
+      const uint32_t b2 = byte_of(w.m[3], i);
+      sc = (b2 & 0x0Fu) | ((b0 >> 6) << 4);
+      mn = (b2 >> 4) | ((b1 >> 6) << 4);
+    } else {
+      sc = b0 & 63u;
+      mn = b1 & 63u;
+    }
+    float d1 = h2f_lo(w.m[0]) * (float)sc, m1 = h2f_hi(w.m[0]) * (float)mn;
+    if (!ok) d1 = m1 = 0.0f;
+    const float b = -fmaf(1024.0f, d1, m1); /* d1 n - m1 */
+    const uint32_t u0 = w.q[0] ^ 0x88888888u, u1 = w.q[1] ^ 0x88888888u;
+    o0 = word_op<BF>(u0 & 0x0F0F0F0Fu, (u0 >> 4) & 0x0F0F0F0Fu, d1, b);
+    o1 = word_op<BF>(u1 & 0x0F0F0F0Fu, (u1 >> 4) & 0x0F0F0F0Fu, d1, b);
+  }
+};
+template <>
+struct QQ<Q6_K> {
+  static constexpr int kLoads = 4;
+  struct Raw { u32x2 ql; uint32_t qh, sc, d; };
+  __device__ static Raw get(const QRes &r, uint32_t row, uint32_t c, uint32_t h) {
+    const uint32_t blk = row * r.nb + (c >> 3);
+    Raw w;
+    w.ql = ql8(r.q, row * r.q_stride + 16u * c + 8u * h);
+    w.qh = ql4(r.aux, row * r.k4 + 8u * c + 4u * h);
+    w.sc = ql2(r.meta, blk * 16u + 2u * (c & 7u)); /* both halves' scales */
+    w.d = ql2(r.d, blk * 2u);
+    return w;
+  }
+  template <int N>
+  __device__ static void wait(Raw &w) {
+    __asm__ volatile("s_waitcnt vmcnt(%4)"
+                     : "+v"(w.ql), "+v"(w.qh), "+v"(w.sc), "+v"(w.d)
+                     : "i"(N));
+  }
+  /* byte = l | h2 << 4 = q (0..63); value = d sc (q - 32) */
+  template <bool BF, int HI>
+  __device__ static void vals(const Raw &w, uint32_t, uint32_t h, bool ok, uint4 &o0, uint4 &o1) {
+    const float d = ok ? h2f((uint16_t)w.d) : 0.0f;
+    const float s = d * (float)(int32_t)(int8_t)(h ? (w.sc >> 8) : w.sc), b = -1056.0f * s;
+    const uint32_t h0 = w.qh & 0x33333333u, h1 = (w.qh >> 2) & 0x33333333u;
+    const uint32_t l0 = w.ql[0] ^ 0x88888888u, l1 = w.ql[1] ^ 0x88888888u;
+    o0 = word_op<BF>(bfi(0xF0F0F0F0u, h0 << 4, l0), bfi(0xF0F0F0F0u, h0, l0 >> 4), s, b);
+    o1 = word_op<BF>(bfi(0xF0F0F0F0u, h1 << 4, l1), bfi(0xF0F0F0F0u, h1, l1 >> 4), s, b);
+  }
+};
+
+template <class F, bool BF>
+__global__ void __launch_bounds__(lg::NT, 1) k_gemm_lds(GemmArgs a) {
+  using namespace lg;
+  __shared__ __attribute__((aligned(16))) uint8_t L[kLds];
+
+  const uint32_t logical = (blockIdx.x % kXcds) * a.per_xcd + blockIdx.x / kXcds;
+  const uint32_t ntile = a.tiles_n * a.tiles_m;
+  if (logical >= ntile * a.splits) return;
+  const uint32_t split = logical / ntile, tile = logical % ntile;
+  const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
+  paik_qview_t v = a.v;
+  float *ybase = a.y;
+  uint32_t tl = tn, rows_before = 0, cum = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMats; ++i) {
+    cum += a.mv[i - 1].n;
+    if ((uint32_t)i < a.count && tn >= a.tile_end[i - 1]) {
+      v = a.mv[i];
+      ybase = a.my[i];
+      tl = tn - a.tile_end[i - 1];
+      rows_before = cum;
+    }
+  }
+  const uint32_t n0 = tl * (uint32_t)BM, m0 = tm * (uint32_t)BN;
+  const uint32_t nchunks = v.k >> 5;
+  const uint32_t s0 = split * a.steps_per_split; /* multiple of 4 */
+  const uint32_t s1 = s0 + a.steps_per_split;
+
+  const int tid = (int)threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t wr = (uint32_t)wave & 1u, wt = (uint32_t)wave >> 1;
+
+  /* dequantization role: row drow of the tile, columns 16 dq .. 16 dq + 15
+   * of each stage (nibble words 2 (dq % 2), +1 of chunk 2 s + dq / 2). A
+   * quarter-wave writes one segment of 16 consecutive rows, which the tile
+   * layout spreads over every LDS bank. */
+  const uint32_t drow = 16u * (uint32_t)wave + ((uint32_t)lane & 15u);
+  const uint32_t dq = (uint32_t)lane >> 4, dh = dq & 1u;
+  const uint32_t grow = min(n0 + drow, v.n - 1u);
+  const QRes res = make_qres(v);
+  using Q = QQ<F>;
+  typedef typename Q::Raw Raw;
+  constexpr int kW = Q::kLoads;
+  auto load_w = [&](uint32_t s, Raw &dst) {
+    dst = Q::get(res, grow, min(2u * s + (dq >> 1), nchunks - 1u), dh);
+  };
+  const uint32_t woff0 = lg_off(drow, 2u * dq), woff1 = lg_off(drow, 2u * dq + 1u);
+  auto deq = [&](auto uu, uint32_t s, Raw &w) {
+    constexpr int U = decltype(uu)::value; /* s % 4 */
+    const uint32_t c = 2u * s + (dq >> 1);
+    uint4 o0, o1;
+    Q::template vals<BF, (U >= 2)>(w, c, dh, c < nchunks, o0, o1);
+    uint8_t *Wt = L + (U & 1) * kWTile;
+    *reinterpret_cast<uint4 *>(Wt + woff0) = o0;
+    *reinterpret_cast<uint4 *>(Wt + woff1) = o1;
+  };
+
+  /* DMA items: instruction u of this wave fills lines 4 (kXDma wave + u) ..
+   * +3 of the activation tile; the lane writes slot lane % 16 of its line,
+   * i.e. token row 2 line + slot % 2, segment (slot / 2) ^ line */
+  const __amdgpu_buffer_rsrc_t xres = plane_rsrc(a.x16, a.x_bytes);
+  uint32_t doff[kXDma], dcol[kXDma];
+#pragma unroll
+  for (int u = 0; u < kXDma; ++u) {
+    const uint32_t line = 4u * (uint32_t)(kXDma * wave + u) + ((uint32_t)lane >> 4);
+    const uint32_t slot = (uint32_t)lane & 15u;
+    const uint32_t row = 2u * line + (slot & 1u), seg = ((slot >> 1) ^ line) & 7u;
+    const uint32_t tok = m0 + row;
+    dcol[u] = 8u * seg;
+    doff[u] = tok < a.m ? (tok * v.k + 8u * seg) * 2u : 0x80000000u;
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)L;
+  auto dma_one = [&](uint32_t s, uint32_t buf, int u, uint32_t off) {
+    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)(
+        lds0 + 2u * kWTile + buf * (uint32_t)kXTile + (uint32_t)(kXDma * wave + u) * 1024u));
+    const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)(2u * KS * s));
+    uint32_t saved;
+    __asm__ volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(dst), "v"(off), "s"(xres), "s"(soff)
+        : "memory");
+  };
+  auto dma_x = [&](uint32_t s, uint32_t buf) {
+    /* a stage inside K needs no per-lane column check (uniform branch) */
+    if ((uint32_t)KS * (s + 1u) <= v.k) {
+#pragma unroll
+      for (int u = 0; u < kXDma; ++u) dma_one(s, buf, u, doff[u]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < kXDma; ++u)
+        dma_one(s, buf, u, (uint32_t)KS * s + dcol[u] < v.k ? doff[u] : 0x80000000u);
+    }
+  };
+
+  /* operand offsets: fragment rows (A: tokens 64 wt + 32 i + lane % 32; B:
+   * rows 64 wr + 32 j + lane % 32), segment 2 sub + lane / 32 */
+  const uint32_t kset = (uint32_t)lane >> 5;
+  uint32_t aoff[2][4], boff[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      aoff[i][u] = lg_off(64u * wt + 32u * (uint32_t)i + ((uint32_t)lane & 31u), 2u * (uint32_t)u + kset);
+      boff[i][u] = lg_off(64u * wr + 32u * (uint32_t)i + ((uint32_t)lane & 31u), 2u * (uint32_t)u + kset);
+    }
+  f16x_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  /* Issue order per stage: DMA (kXDma), then weight loads (kW). Waits:
+   * weights of stage s+1 before their dequantization (all but the last
+   * 3 kW + 2 kXDma requests), activations of stage s+1 before the barrier
+   * (all but the last 2 kW + kXDma). The prologue issues X(s0), W(s0..s0+2),
+   * X(s0+1), W(s0+3), for which the same counts hold. */
+  Raw ring[kRing];
+  dma_x(s0, 0u);
+  load_w(s0, ring[0]);
+  load_w(s0 + 1u, ring[1]);
+  load_w(s0 + 2u, ring[2]);
+  dma_x(s0 + 1u, 1u);
+  load_w(s0 + 3u, ring[3]);
+  Q::template wait<3 * kW + kXDma>(ring[0]);
+  deq(std::integral_constant<int, 0>(), s0, ring[0]);
+  __syncthreads();
+
+  auto body = [&](auto uu, uint32_t s) {
+    constexpr int U = decltype(uu)::value; /* s % 4 (s0 % 4 == 0) */
+    dma_x(s + 2u, (uint32_t)((U + 2) & 3));
+    load_w(s + 4u, ring[U]);
+    const uint8_t *Xt = L + 2 * kWTile + U * kXTile;
+    const uint8_t *Wt = L + (U & 1) * kWTile;
+    /* operands of sub-step u + 1 are read before the MFMAs of sub-step u */
+    uint4 Ac[2], Bc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      Ac[i] = *reinterpret_cast<const uint4 *>(Xt + aoff[i][0]);
+      Bc[i] = *reinterpret_cast<const uint4 *>(Wt + boff[i][0]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint4 An[2], Bn[2];
+      if (u < 3) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          An[i] = *reinterpret_cast<const uint4 *>(Xt + aoff[i][u + 1]);
+          Bn[i] = *reinterpret_cast<const uint4 *>(Wt + boff[i][u + 1]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma<BF>(Ac[i], Bc[j], acc[i][j]);
+      if (u == 1) {
+        Q::template wait<3 * kW + 2 * kXDma>(ring[(U + 1) & 3]);
+        deq(std::integral_constant<int, (U + 1) & 3>(), s + 1u, ring[(U + 1) & 3]);
+      }
+      if (u < 3) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          Ac[i] = An[i];
+          Bc[i] = Bn[i];
+        }
+      }
+    }
+    wait_vmem<2 * kW + kXDma>();
+    __syncthreads();
+  };
+  for (uint32_t s = s0; s < s1; s += 4u) {
+    body(std::integral_constant<int, 0>(), s);
+    body(std::integral_constant<int, 1>(), s + 1u);
+    body(std::integral_constant<int, 2>(), s + 2u);
+    body(std::integral_constant<int, 3>(), s + 3u);
+  }
+  /* The last iteration's ring loads are never used: wait for them with
+   * their registers bound, so none is reused while a load may still write
+   * it, and no DMA lands in LDS after the workgroup ends. */
+#pragma unroll
+  for (int i = 0; i < kRing; ++i) Q::template wait<0>(ring[i]);
+
+  /* lane (r, g) holds row 64 wr + 32 j + r for tokens 8 (e / 4) + 4 g + e % 4
+   * of fragment i */
+  const bool split_k = a.splits > 1u;
+  const bool gated = a.gate != nullptr && !split_k;
+  float *const pbase = a.part != nullptr ? a.part + (size_t)a.splits * a.m * rows_before +
+                                                (size_t)split * a.m * v.n
+                                          : nullptr;
+  const uint32_t r = (uint32_t)lane & 31u, g = (uint32_t)lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t row = n0 + 64u * wr + 32u * (uint32_t)j + r;
+      const uint32_t t0 = m0 + 64u * wt + 32u * (uint32_t)i + 4u * g;
+      float gv[16];
+      if (gated) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t tok = min(t0 + 8u * (uint32_t)(e >> 2) + (uint32_t)(e & 3), a.m - 1u);
+          gv[e] = a.gate[(size_t)tok * v.n + min(row, v.n - 1u)];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t tok = t0 + 8u * (uint32_t)(e >> 2) + (uint32_t)(e & 3);
+        if (tok < a.m && row < v.n) {
+          const size_t at = (size_t)tok * v.n + row;
+          const float val = acc[i][j][e];
+          if (pbase != nullptr) pbase[at] = val;
+          else if (split_k) unsafeAtomicAdd(ybase + at, val);
+          else if (gated) ybase[at] = silu_mul(gv[e], val);
+          else ybase[at] = val;
+        }
+      }
+    }
+}
+
+/* Grid of a k_gemm_lds launch: 128-row x 256-token tiles; K split while
+ * the tiles leave most CUs idle, each part at least 16 stages (1024
+ * columns), the stage count per part a multiple of 4. */
+static void plan_lds(GemmArgs &a) {
+  if (a.count <= 1u) a.tiles_n = (a.v.n + lg::BM - 1u) / lg::BM;
+  a.tiles_m = (a.m + lg::BN - 1u) / lg::BN;
+  const uint32_t tiles = a.tiles_n * a.tiles_m;
+  const uint32_t nst = ((a.v.k + lg::KS - 1u) / lg::KS + 3u) & ~3u;
+  uint32_t splits = 1;
+  while (tiles * splits * 2u <= 256u && nst / (splits * 2u) >= 16u) splits *= 2u;
+  if (paik_tune.gemm_splits >= 1 && paik_tune.gemm_splits <= 64)
+    splits = (uint32_t)paik_tune.gemm_splits;
+  if (a.gate != nullptr) splits = 1u;
+  a.steps_per_split = ((nst + splits - 1u) / splits + 3u) & ~3u;
+  a.splits = (nst + a.steps_per_split - 1u) / a.steps_per_split;
+  a.per_xcd = (tiles * a.splits + kXcds - 1u) / kXcds;
+}
+
+/* TT = 0: the LDS-shared prefill kernel (k_gemm_lds); otherwise k_gemm_x16
+ * with that tile. */
 template <class F, int TT, int NW, int RWG>
 static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
                              uint32_t m, const float *x, uint16_t *x16, const float *gate,
                              bool bf16, float *part, size_t part_bytes, bool silu_pair,
                              hipStream_t s) {
+  constexpr uint32_t kRows = TT == 0 ? (uint32_t)lg::BM : (uint32_t)RWG;
   const paik_qview_t &v = *vs[0];
   hipError_t e = hipSuccess;
   if (x != nullptr) { /* x == nullptr: x16 already holds these tokens */
@@ -939,11 +1389,12 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
   for (uint32_t i = 0; i < count; ++i) {
     a.mv[i] = *vs[i];
     a.my[i] = ys[i];
-    tiles += (vs[i]->n + (uint32_t)RWG - 1u) / (uint32_t)RWG;
+    tiles += (vs[i]->n + kRows - 1u) / kRows;
     a.tile_end[i] = tiles;
   }
   a.tiles_n = tiles;
-  plan_grid(a, RWG, TT);
+  if constexpr (TT == 0) plan_lds(a);
+  else plan_grid(a, RWG, TT);
   a.x_bytes = (uint32_t)((size_t)m * v.k * 2u);
   size_t rows = 0;
   uint32_t ns[kGemmMats];
@@ -962,12 +1413,34 @@ static hipError_t launch_x16(const paik_qview_t *const *vs, float *const *ys, ui
       if (e != hipSuccess) return e;
     }
   }
-  const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
-  if (bf16) k_gemm_x16<F, true, TT, NW, RWG><<<grid, block, 0, s>>>(a);
-  else k_gemm_x16<F, false, TT, NW, RWG><<<grid, block, 0, s>>>(a);
+  const dim3 grid(a.per_xcd * kXcds);
+  if constexpr (TT == 0) {
+    if (bf16) k_gemm_lds<F, true><<<grid, dim3(lg::NT), 0, s>>>(a);
+    else k_gemm_lds<F, false><<<grid, dim3(lg::NT), 0, s>>>(a);
+  } else {
+    if (bf16) k_gemm_x16<F, true, TT, NW, RWG><<<grid, dim3(64 * NW), 0, s>>>(a);
+    else k_gemm_x16<F, false, TT, NW, RWG><<<grid, dim3(64 * NW), 0, s>>>(a);
+  }
   e = hipGetLastError();
   if (e != hipSuccess || !parts) return e;
   return launch_reduce(part, ys, ns, count, m, a.splits, s, silu_pair);
+}
+
+/* The 16-bit kernel a block of mt tokens of format `type` runs on:
+ *   1  k_gemm_x16, 32-token x 256-row tiles (up to 32 tokens)
+ *   2  k_gemm_x16, 128-token x 256-row tiles on 8 waves
+ *   3  k_gemm_x16, 256-token x 128-row tiles on 4 waves (measurement only)
+ *   4  k_gemm_lds (Q6_K from 256 tokens)
+ * Measured at 512 tokens (gate 14336 x 4096 / down 4096 x 14336): Q4_K
+ * 81 / -, Q4_0 82, Q8_0 96 us on tiles 2; Q6_K down 118.9 us on 4 against
+ * 126.6 on 2 and 121.1 on 3; from 1024 tokens the order holds. The
+ * gemm_tile tuning field overrides the choice. */
+static int pick_kind(uint32_t type, uint32_t mt) {
+  const int t = paik_tune.gemm_tile;
+  if (t >= 1 && t <= 4) return t;
+  if (mt <= 32u) return 1;
+  if (mt < 256u || type != 14u) return 2;
+  return 4;
 }
 
 template <class F>
@@ -994,18 +1467,19 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
     float *yt[kGemmMats];
     for (uint32_t i = 0; i < count; ++i) yt[i] = ys[i] + (size_t)t0 * vs[i]->n;
     const float *gt = gate != nullptr ? gate + (size_t)t0 * v.n : nullptr;
-    /* up to 32 tokens: 32-token tiles; up to 255: 128 x 256 tiles on 8
-     * waves; from 256 tokens: 256 x 128 tiles on 4 waves (each weight
-     * value dequantized once per 256 tokens). The 16-bit path takes all
-     * matrices in one launch; the register-staged path one per matrix. */
+    /* The 16-bit path takes all matrices in one launch (kernel by
+     * pick_kind); the register-staged path one per matrix. */
     hipError_t e = hipSuccess;
     if (use16) {
-      e = mt <= 32u    ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+      const int kind = pick_kind(F::kType, mt);
+      e = kind == 1   ? launch_x16<F, 32, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+                                                  part_bytes, silu_pair, s)
+          : kind == 2 ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
                                                    part_bytes, silu_pair, s)
-          : mt < 256u ? launch_x16<F, 128, 8, 256>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+          : kind == 3 ? launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, part,
                                                    part_bytes, silu_pair, s)
-                      : launch_x16<F, 256, 4, 128>(vs, yt, count, mt, xt, x16, gt, bf16, part,
-                                                   part_bytes, silu_pair, s);
+                      : launch_x16<F, 0, 8, 0>(vs, yt, count, mt, xt, x16, gt, bf16, part,
+                                               part_bytes, silu_pair, s);
     } else {
       if (silu_pair) return hipErrorInvalidValue; /* the pair form needs the 16-bit path */
       for (uint32_t i = 0; i < count && e == hipSuccess; ++i)
@@ -1074,9 +1548,12 @@ extern "C" uint32_t paik_gemm_x16_splits(const paik_qview_t *v, uint32_t m) {
   memset(&a, 0, sizeof a);
   a.v = *v;
   a.m = m;
-  if (m <= 32u) plan_grid(a, 256u, 32u);
-  else if (m < 256u) plan_grid(a, 256u, 128u);
-  else plan_grid(a, 128u, 256u);
+  switch (pick_kind(v->type, m)) {
+  case 1: plan_grid(a, 256u, 32u); break;
+  case 2: plan_grid(a, 256u, 128u); break;
+  case 3: plan_grid(a, 128u, 256u); break;
+  default: plan_lds(a); break;
+  }
   return a.splits;
 }
 extern "C" uint64_t paik_gemm_part_bytes(const paik_qview_t *const *vs, uint32_t count,
@@ -1087,14 +1564,16 @@ extern "C" uint64_t paik_gemm_part_bytes(const paik_qview_t *const *vs, uint32_t
   a.v = *vs[0];
   a.m = m;
   a.count = count;
-  const uint32_t tt = m <= 32u ? 32u : m < 256u ? 128u : 256u;
-  const uint32_t rwg = m < 256u ? 256u : 128u;
+  const int kind = pick_kind(vs[0]->type, m);
+  const uint32_t tt = kind == 1 ? 32u : kind == 2 ? 128u : 256u;
+  const uint32_t rwg = kind == 3 ? 128u : kind == 4 ? (uint32_t)lg::BM : 256u;
   uint64_t rows = 0;
   for (uint32_t i = 0; i < count; ++i) {
     a.tiles_n += (vs[i]->n + rwg - 1u) / rwg;
     rows += vs[i]->n;
   }
-  plan_grid(a, rwg, tt);
+  if (kind == 4) plan_lds(a);
+  else plan_grid(a, rwg, tt);
   return a.splits > 1u ? (uint64_t)a.splits * m * rows * 4u : 0u;
 }
 #endif

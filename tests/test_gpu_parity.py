@@ -265,8 +265,11 @@ def test_mfma_forced_split_k_ragged(splits):
 @pytest.mark.parametrize("m", [40, 300])
 def test_mfma_16bit_copy_matches_register_staging(qtype, m):
     """The activations reach LDS either from the matrix's 16-bit workspace
-    (DMA) or through registers; both round x the same way and accumulate in
-    the same order, so the outputs are identical."""
+    (DMA) or through registers; both round x and the weights the same way.
+    Below 256 tokens both kernels also accumulate in the same order, so the
+    outputs are identical; from 256 tokens the workspace path runs the
+    LDS-shared prefill kernel, whose MFMAs group the columns differently:
+    the f32 sums agree to rel-L2 1e-5."""
     n, k = 300, 32 * 37 if QK[qtype] == 32 else 256 * 5
     say(f"[gpu] gemm MFMA x16 vs registers type={qtype} m={m}")
     blocks = weights(qtype, n, k, 120 + qtype)
@@ -275,7 +278,10 @@ def test_mfma_16bit_copy_matches_register_staging(qtype, m):
     y16 = qm.gemm(x)
     with pa.tuning(gemm_no_x16=1):
         yreg = qm.gemm(x)
-    assert np.array_equal(y16, yreg)
+    if m < 256:
+        assert np.array_equal(y16, yreg)
+    else:
+        assert rel_l2(y16, yreg) <= 1e-5
     assert rel_l2(y16, ob.qgemm_f64(qtype, n, k, blocks, x)) <= TOL_F16
 
 
