@@ -313,6 +313,62 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate,
 pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags);
 
 /* ---------------------------------------------------------------------- */
+/* CPU reference twin                                                       */
+/* ---------------------------------------------------------------------- */
+
+/* y[m][n] = x[m][k] * W^T on the host, W[N][K] given as native GGUF blocks
+ * (`blocks`, N rows of K/blk blocks) of `type`: the reference's CPU
+ * composition for such a weight, pai_gguf_dequant (adapters/llama/
+ * gguf.c:650-947) then pai_ref_gemm_f32 on the transposed values
+ * (cpu/reference/ref_ops.c:427-444), bit for bit. Argument order follows
+ * pai_ref_gemm_f32 (m, n, k, a, b, c) with the format first. This is the
+ * ref_fn of the qgemm_* descriptors (PAI_OP_CAP_CPU_REF), which the
+ * reference's executor requires of every op it schedules
+ * (scheduler/scheduler.c:749-756); no GPU entry point calls it, and it
+ * allocates nothing. Errors: INVALID_ARG (NULL, zero dims), UNSUPPORTED
+ * (type, or K not a whole number of blocks). */
+pai_status_t pai_qgemm_ref_f32(uint32_t type, uint64_t m, uint64_t n,
+                               uint64_t k, const float *x, const void *blocks,
+                               float *y);
+
+/* ---------------------------------------------------------------------- */
+/* IR quantization tag of GGUF block weights                                */
+/* ---------------------------------------------------------------------- */
+
+/* The block structure a GGUF-tagged IR value carries: one more value of
+ * pai_ir_quant_block_t (ir/ir.h:88-93), after PAI_IR_QUANT_BLOCK_GROUP,
+ * so PAI_IR_QUANT_BLOCK_COUNT becomes 4 and pai_ir_value_set_quant
+ * (ir/ir.c:62-80) accepts it unchanged otherwise. */
+#define PAI_IR_QUANT_BLOCK_GGUF 3u
+
+/* Same field order, types and size as pai_ir_quant_t (ir/ir.h:95-103); the
+ * repr fields hold pai_ir_quant_repr_t values (0 = F32, 1 = F16). */
+typedef struct pai_hip_ir_quant {
+  uint8_t present;
+  uint8_t bit_width;
+  uint8_t scale_repr;
+  uint8_t zero_point_repr;
+  uint8_t is_signed;
+  uint8_t block_structure;
+  uint16_t group_size;
+} pai_hip_ir_quant_t;
+
+/* The tag of a block format: block_structure PAI_IR_QUANT_BLOCK_GGUF and
+ *   Q8_0  8 bits, signed,   group 32,  f16 scale
+ *   Q4_0  4 bits, unsigned, group 32,  f16 scale (codes offset by 8)
+ *   Q4_K  4 bits, unsigned, group 256, f16 scale, f16 min (zero-point repr)
+ *   Q6_K  6 bits, signed,   group 256, f16 scale (int8 sub-scales)
+ * (bit_width, group_size, is_signed) tells the four apart. UNSUPPORTED for
+ * other types, INVALID_ARG for NULL. No counterpart in the reference,
+ * whose importer dequantizes GGUF weights instead of tagging them
+ * (adapters/llama/llama.c:408-470). */
+pai_status_t pai_hip_quant_tag(uint32_t type, pai_hip_ir_quant_t *out);
+
+/* The ggml type id a tag denotes (PAI_QTYPE_*), or 0 when the tag is NULL,
+ * absent, not GGUF-structured, or none of the four formats. */
+uint32_t pai_hip_quant_type(const pai_hip_ir_quant_t *q);
+
+/* ---------------------------------------------------------------------- */
 /* Op-registry descriptors                                                  */
 /* ---------------------------------------------------------------------- */
 
@@ -338,12 +394,12 @@ typedef struct pai_hip_op_descriptor {
   uint32_t reserved[2];
 } pai_hip_op_descriptor_t;
 
-/* The four GPU descriptors "qgemm_q4_0_f32", "qgemm_q8_0_f32",
+/* The four descriptors "qgemm_q4_0_f32", "qgemm_q8_0_f32",
  * "qgemm_q4_k_f32", "qgemm_q6_k_f32" (inputs: x f32, packed weight u8;
- * output y f32; caps PAI_OP_CAP_GPU_HIP; ref_fn NULL, because the CPU
- * path for these weights stays the reference's own dequant-at-import
- * followed by pai_ref_gemm_f32; kernel_id PAI_KERNEL_NONE). The array is
- * static and outlives any registry it is registered into. */
+ * output y f32; caps PAI_OP_CAP_CPU_REF | PAI_OP_CAP_GPU_HIP; ref_fn
+ * pai_qgemm_ref_f32, which the dispatch site casts to that prototype, as
+ * it casts the builtins' ref_fn to theirs; kernel_id PAI_KERNEL_NONE). The
+ * array is static and outlives any registry it is registered into. */
 const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count);
 
 /* Registry name for a ggml type ("qgemm_q4_k_f32"), NULL if unsupported. */

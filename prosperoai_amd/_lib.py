@@ -53,6 +53,10 @@ SIGNATURES = {
     "pai_gguf_dir_blocks": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_void_p),
                                         C.POINTER(C.c_uint64)]),
     "pai_qmat_upload_gguf": (C.c_int32, [C.POINTER(C.c_void_p), _vp, C.c_char_p]),
+    "pai_qgemm_ref_f32": (C.c_int32, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, _vp, _vp,
+                                      _vp]),
+    "pai_hip_quant_tag": (C.c_int32, [C.c_uint32, _vp]),
+    "pai_hip_quant_type": (C.c_uint32, [_vp]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),
     "pai_hip_op_name": (C.c_char_p, [C.c_uint32]),
     # pai_llama.h

@@ -23,7 +23,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c"]
+C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c", "pai_qref.c"]
 HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemv_mx.hip", "qgemm.hip", "qdecode.hip",
                "qscratch.hip"]
 # qgemm.hip is also compiled once per block format (object name, defines):
@@ -33,7 +33,10 @@ HIP_VARIANTS = [(f"qgemm_{f.lower()}.hip", "qgemm.hip",
                 for f in ("Q4_K", "Q6_K", "Q4_0", "Q8_0")]
 HEADERS = ["paik.h", "qdev.h"]
 
-C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+# no floating-point contraction: the CPU twin reproduces the reference's
+# separately rounded products and sums
+C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra",
+           "-Wno-unused-parameter",
            "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", f"-I{ROOT / 'include'}",
            f"-I{CSRC}"]
 HIP_FLAGS = ["-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",

@@ -735,11 +735,14 @@ pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags) {
 /* Registry descriptors                                                     */
 /* ---------------------------------------------------------------------- */
 
+/* caps: PAI_OP_CAP_CPU_REF (sdk/include/pai/op.h:59) | PAI_OP_CAP_GPU_HIP */
+#define PAI_QGEMM_CAPS ((1u << 0) | PAI_OP_CAP_GPU_HIP)
+#define PAI_QGEMM_REF ((pai_status_t(*)(void))pai_qgemm_ref_f32)
 static const pai_hip_op_descriptor_t k_ops[] = {
-    {"qgemm_q4_0_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
-    {"qgemm_q8_0_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
-    {"qgemm_q4_k_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
-    {"qgemm_q6_k_f32", 1u, 2u, 1u, 0, 0, PAI_OP_CAP_GPU_HIP, NULL, 0, {0u, 0u}},
+    {"qgemm_q4_0_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
+    {"qgemm_q8_0_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
+    {"qgemm_q4_k_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
+    {"qgemm_q6_k_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
 };
 
 const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count) {
@@ -755,4 +758,47 @@ const char *pai_hip_op_name(uint32_t type) {
   case PAI_QTYPE_Q6_K: return k_ops[3].name;
   default: return NULL;
   }
+}
+
+/* ---------------------------------------------------------------------- */
+/* IR quantization tag                                                      */
+/* ---------------------------------------------------------------------- */
+
+/* (type, bits, signed, group, zero-point repr) of the four formats; the
+ * scale repr is f16 (1) for all. */
+static const struct {
+  uint32_t type;
+  uint8_t bits, is_signed, zp_repr;
+  uint16_t group;
+} k_tags[] = {
+    {PAI_QTYPE_Q8_0, 8u, 1u, 0u, 32u},
+    {PAI_QTYPE_Q4_0, 4u, 0u, 0u, 32u},
+    {PAI_QTYPE_Q4_K, 4u, 0u, 1u, 256u},
+    {PAI_QTYPE_Q6_K, 6u, 1u, 0u, 256u},
+};
+
+pai_status_t pai_hip_quant_tag(uint32_t type, pai_hip_ir_quant_t *out) {
+  if (out == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL argument");
+  for (size_t i = 0; i < sizeof k_tags / sizeof k_tags[0]; ++i) {
+    if (k_tags[i].type != type) continue;
+    memset(out, 0, sizeof *out);
+    out->present = 1u;
+    out->bit_width = k_tags[i].bits;
+    out->scale_repr = 1u; /* PAI_IR_QUANT_REPR_F16 */
+    out->zero_point_repr = k_tags[i].zp_repr;
+    out->is_signed = k_tags[i].is_signed;
+    out->block_structure = (uint8_t)PAI_IR_QUANT_BLOCK_GGUF;
+    out->group_size = k_tags[i].group;
+    return PAI_OK;
+  }
+  return fail(PAI_ERR_UNSUPPORTED, "ggml type %u has no GGUF tag here", type);
+}
+
+uint32_t pai_hip_quant_type(const pai_hip_ir_quant_t *q) {
+  if (q == NULL || q->present == 0u || q->block_structure != PAI_IR_QUANT_BLOCK_GGUF) return 0u;
+  for (size_t i = 0; i < sizeof k_tags / sizeof k_tags[0]; ++i)
+    if (k_tags[i].bits == q->bit_width && k_tags[i].group == q->group_size &&
+        k_tags[i].is_signed == q->is_signed)
+      return k_tags[i].type;
+  return 0u;
 }

@@ -84,8 +84,10 @@ def test_descriptors_layout_and_names():
     assert [d.name.decode() for d in ds] == ["qgemm_q4_0_f32", "qgemm_q8_0_f32",
                                              "qgemm_q4_k_f32", "qgemm_q6_k_f32"]
     for d in ds:
-        assert d.caps == 1 << 3 and d.num_inputs == 2 and d.num_outputs == 1
-        assert d.ref_fn is None and d.kernel_id == 0 and d.in_dtype == 0
+        assert d.caps == (1 << 0) | (1 << 3) and d.num_inputs == 2 and d.num_outputs == 1
+        # the CPU twin, pai_qgemm_ref_f32, is every descriptor's reference function
+        twin = C.cast(pa.lib().pai_qgemm_ref_f32, C.c_void_p).value
+        assert d.ref_fn == twin and d.kernel_id == 0 and d.in_dtype == 0
     # pai_op_descriptor_t is 56 bytes on LP64 (sdk/include/pai/op.h:71-82)
     assert C.sizeof(HipDescriptor) == 56
     assert HipDescriptor.ref_fn.offset == 32 and HipDescriptor.kernel_id.offset == 40
@@ -96,7 +98,8 @@ def test_descriptors_layout_and_names():
 
 def test_descriptors_register_into_reference_registry(ref_lib):
     """Our descriptors, passed by pointer to the reference's own
-    pai_op_registry_register, resolve by name and advertise the HIP cap."""
+    pai_op_registry_register, resolve by name and advertise the HIP and
+    CPU-reference caps (the executor's plan check requires the latter)."""
     reg = C.create_string_buffer(8 + 8 * 64)  # pai_op_registry_t
     assert ref_lib.pai_op_registry_builtin(reg) == 0
     base = ref_lib.pai_op_registry_count(reg)
@@ -109,7 +112,7 @@ def test_descriptors_register_into_reference_registry(ref_lib):
         d = ref_lib.pai_op_registry_lookup(reg, name)
         assert d is not None
         assert ref_lib.pai_op_supports(d, 1 << 3) == 1
-        assert ref_lib.pai_op_supports(d, 1 << 0) == 0  # no CPU ref on this descriptor
+        assert ref_lib.pai_op_supports(d, 1 << 0) == 1
     assert ref_lib.pai_op_registry_lookup(reg, b"matmul_f32") is not None
 
 
