@@ -297,6 +297,11 @@ def prefill(pa, hm, reps: int) -> dict:
     for w in mats:
         w.free()
     x.free(); h.free()
+    g = out["gate_q4_k"]
+    out["roofline"] = {"bound": "mfma", "achieved": g["TFLOPs"], "peak": MFMA_F16_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": g["frac_mfma_f16"], "traffic": None,
+                       "workload": "gate Q4_K 14336x4096 at M=512 (one call: activation "
+                                   "conversion + GEMM, HIP events around graph-captured calls)"}
     return out
 
 
@@ -547,6 +552,52 @@ def pmc_summary(fetch_csv: str, write_csv: str, copy_mib: int, kernel: str) -> d
             "traffic_bytes_per_launch": round(f_b * f_s + w_b * w_s)}
 
 
+def kernel_pmc_summary(paths: list) -> dict:
+    """Per-kernel means of rocprofv3 --pmc CSVs (counter_collection): the
+    dispatch count, the duration between each dispatch's start and end
+    timestamps, and every counter's mean per dispatch. With
+    SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE in the same pass, MFMA busy
+    = SIMD cycles with an MFMA in flight / (GPU cycles x 1024 SIMDs), where
+    GPU cycles = GRBM_GUI_ACTIVE / 8 (the counter is summed over the 8
+    XCDs); with the MOPS counters, flops = MOPS x 512."""
+    import csv
+    out = {}
+    for path in paths:
+        per = {}
+        for r in csv.DictReader(open(path)):
+            d = per.setdefault(r["Dispatch_Id"], {"kernel": r["Kernel_Name"].split("(")[0],
+                                                  "grid": int(r["Grid_Size"]),
+                                                  "ns": int(r["End_Timestamp"]) -
+                                                        int(r["Start_Timestamp"])})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for d in per.values():
+            key = f"{d['kernel']} grid={d['grid']}"
+            e = out.setdefault(key, {"file": path, "dispatches": 0, "sums": {}})
+            if e["file"] != path:
+                key = f"{key} [{Path(path).parent.name}]"
+                e = out.setdefault(key, {"file": path, "dispatches": 0, "sums": {}})
+            e["dispatches"] += 1
+            for c, v in d.items():
+                if c not in ("kernel", "grid"):
+                    e["sums"][c] = e["sums"].get(c, 0.0) + v
+    for e in out.values():
+        mean = {c: v / e["dispatches"] for c, v in e.pop("sums").items()}
+        e["mean_us"] = round(mean.pop("ns") / 1e3, 2)
+        e["counters"] = {c: round(v, 1) for c, v in mean.items()}
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "GRBM_GUI_ACTIVE" in mean:
+            cyc = mean["GRBM_GUI_ACTIVE"] / 8.0
+            e["gpu_cycles"] = round(cyc)
+            e["clock_GHz"] = round(cyc / (e["mean_us"] * 1e3), 3)
+            e["mfma_busy"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * 1024.0), 4)
+        mops = mean.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + mean.get(
+            "SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        if mops:
+            e["mfma_flop"] = mops * 512.0
+            e["TFLOPs"] = round(mops * 512.0 / (e["mean_us"] * 1e-6) / 1e12, 1)
+            e["frac_mfma_f16"] = round(e["TFLOPs"] / MFMA_F16_PEAK_TFLOPS, 4)
+    return out
+
+
 def trace_summary(trace_csv: str, steps: int, warmup: int, layers: int) -> dict:
     """Kernel durations of the headline's timed region from a rocprofv3
     --kernel-trace CSV of a default run: the first Q4_0 GEMV dispatches are
@@ -600,6 +651,14 @@ def main() -> int:
     ap.add_argument("--decode-only", type=int, metavar="STEPS", default=0,
                     help="run only the full-model decode step (Llama-3-8B shape, fp16 KV "
                          "cache at context 2048) for STEPS timed steps and print its JSON")
+    ap.add_argument("--prefill-only", type=int, metavar="REPS", default=0,
+                    help="run only the M=512 prefill GEMMs (REPS graph-captured calls per "
+                         "shape) and print their JSON")
+    ap.add_argument("--kernel-pmc-summary", nargs="+", metavar="PMC_CSV",
+                    help="per-kernel durations and counter means of rocprofv3 --pmc CSVs, "
+                         "then exit")
+    ap.add_argument("--pmc-kernel", default="k_gemv<paik::Q4_0",
+                    help="kernel-name substring for --pmc-summary")
     ap.add_argument("--trace-summary", metavar="TRACE_CSV",
                     help="summarise the headline's timed-region GEMV dispatches of a "
                          "rocprofv3 --kernel-trace CSV of a run with the same --steps, "
@@ -614,7 +673,10 @@ def main() -> int:
         return 0
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, args.calib_copy_mib or 64,
-                                     "k_gemv<paik::Q4_0")))
+                                     args.pmc_kernel)))
+        return 0
+    if args.kernel_pmc_summary:
+        print(json.dumps(kernel_pmc_summary(args.kernel_pmc_summary), indent=1))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -626,6 +688,11 @@ def main() -> int:
     pa.init()
     if args.decode_only:
         print(json.dumps(decode_8b(pa, hm, args.decode_only, 5)), flush=True)
+        return 0
+    if args.prefill_only:
+        print(json.dumps(prefill(pa, hm, args.prefill_only)), flush=True)
+        if args.calib_copy_mib:
+            copy_calibration(hm, args.calib_copy_mib)
         return 0
     log(f"Q4_0 M=1 x {args.layers} layers")
 
