@@ -528,6 +528,147 @@ ORC_AVX2 int32_t orc_opt_gemm_w8_avx2(uint64_t m, uint64_t n, uint64_t k,
 }
 
 /* ---------------------------------------------------------------------- */
+/* v0 per-group schemes (models/quantize.c) and the GEMMs over them       */
+/* (cpu/reference/ref_ops.c:446-499)                                      */
+/* ---------------------------------------------------------------------- */
+
+/* models/quantize.c:6-26: 4 or 8 bits, signed only; group size 0 means
+ * one group over all n elements. */
+int32_t orc_quant_group_size(const orc_quant_scheme_t *s, uint64_t n, uint64_t *out_gs) {
+  if (s == NULL) return ORC_ERR_INVALID_ARG;
+  if (s->bit_width != 8u && s->bit_width != 4u) return ORC_ERR_UNSUPPORTED;
+  if (!s->is_signed) return ORC_ERR_UNSUPPORTED;
+  const uint64_t gs = s->group_size == 0u ? n : (uint64_t)s->group_size;
+  if (gs == 0u) return ORC_ERR_INVALID_ARG;
+  *out_gs = gs;
+  return ORC_OK;
+}
+
+/* models/quantize.c:34-49 */
+uint64_t orc_quant_num_groups(uint64_t n, const orc_quant_scheme_t *s) {
+  uint64_t gs;
+  if (s == NULL || n == 0u || orc_quant_group_size(s, n, &gs) != ORC_OK) return 0u;
+  return n / gs + (n % gs != 0u ? 1u : 0u);
+}
+
+/* models/quantize.c:51-60 (no scheme validation there either) */
+uint64_t orc_quant_value_bytes(uint64_t n, const orc_quant_scheme_t *s) {
+  if (s == NULL || n == 0u) return 0u;
+  return s->bit_width == 4u ? (n + 1u) / 2u : n;
+}
+
+/* models/quantize.c:74-141: per group, scale = max|x| / qmax (127 or 7),
+ * q = lrintf(x / scale) clamped to [-qmax, qmax] (0 for a zero group);
+ * 4-bit codes go two per byte, element 2i in the low nibble. */
+int32_t orc_quantize_v0_f32(const float *src, uint64_t n, const orc_quant_scheme_t *s,
+                            int8_t *out_q, float *out_scales, uint64_t *out_groups) {
+  if (src == NULL || out_q == NULL || out_scales == NULL) return ORC_ERR_INVALID_ARG;
+  uint64_t gs;
+  const int32_t st = orc_quant_group_size(s, n, &gs);
+  if (st != ORC_OK) return st;
+  const int32_t qmax = s->bit_width == 8u ? 127 : 7;
+  memset(out_q, 0, (size_t)orc_quant_value_bytes(n, s));
+  uint64_t g = 0;
+  for (uint64_t t = 0; t < n; ++g, t += gs) {
+    const uint64_t t1 = t + gs < n ? t + gs : n;
+    float max_abs = 0.0f;
+    for (uint64_t i = t; i < t1; ++i) {
+      const float av = fabsf(src[i]);
+      if (av > max_abs) max_abs = av;
+    }
+    const float scale = max_abs > 0.0f ? max_abs / (float)qmax : 0.0f;
+    out_scales[g] = scale;
+    for (uint64_t i = t; i < t1; ++i) {
+      int32_t q = 0;
+      if (scale > 0.0f) {
+        q = (int32_t)lrintf(src[i] / scale);
+        q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
+      }
+      if (s->bit_width == 4u) {
+        uint8_t *byte = (uint8_t *)out_q + i / 2u;
+        const uint8_t nib = (uint8_t)(q & 0x0F);
+        *byte = (i & 1u) == 0u ? (uint8_t)((*byte & 0xF0u) | nib) : (uint8_t)((*byte & 0x0Fu) | (nib << 4));
+      } else {
+        out_q[i] = (int8_t)q;
+      }
+    }
+  }
+  if (out_groups != NULL) *out_groups = g;
+  return ORC_OK;
+}
+
+/* The signed 4-bit value of element `flat` of a nibble array (low nibble
+ * for even indices; ref_ops.c:487-490, quantize.c:167-171). */
+static inline int32_t nibble_at(const int8_t *q4, uint64_t flat) {
+  const uint8_t byte = (uint8_t)q4[flat / 2u];
+  const int32_t nib = (flat & 1u) == 0u ? (byte & 0x0F) : (byte >> 4);
+  return (nib & 0x08) ? nib - 16 : nib;
+}
+
+/* models/quantize.c:143-181: out[i] = scale * (float)q */
+int32_t orc_dequantize_v0_f32(const int8_t *q, const float *scales, uint64_t n,
+                              const orc_quant_scheme_t *s, float *out) {
+  if (q == NULL || scales == NULL || out == NULL) return ORC_ERR_INVALID_ARG;
+  uint64_t gs;
+  const int32_t st = orc_quant_group_size(s, n, &gs);
+  if (st != ORC_OK) return st;
+  uint64_t g = 0;
+  for (uint64_t t = 0; t < n; ++g, t += gs) {
+    const uint64_t t1 = t + gs < n ? t + gs : n;
+    const float scale = scales[g];
+    for (uint64_t i = t; i < t1; ++i)
+      out[i] = scale * (float)(s->bit_width == 4u ? nibble_at(q, i) : (int32_t)q[i]);
+  }
+  return ORC_OK;
+}
+
+/* cpu/reference/ref_ops.c:446-468 (bits 8) and :470-499 (bits 4):
+ * c[i][j] = sum over t ascending of (a[i][t] * q(t, j)) * scale[t/gs][j],
+ * q(t, j) at flat index t*n+j; group size 0 or > k means one group. */
+int32_t orc_gemm_wq_seq_f32(uint32_t bits, uint64_t m, uint64_t n, uint64_t k, const float *a,
+                            const int8_t *w_q, const float *b_scales, uint64_t group_size,
+                            float *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || w_q == NULL || b_scales == NULL || c == NULL)
+    return ORC_ERR_INVALID_ARG;
+  if (bits != 8u && bits != 4u) return ORC_ERR_UNSUPPORTED;
+  const uint64_t gs = (group_size == 0u || group_size > k) ? k : group_size;
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (uint64_t t = 0; t < k; ++t) {
+        const uint64_t flat = t * n + j;
+        const int32_t qv = bits == 4u ? nibble_at(w_q, flat) : (int32_t)w_q[flat];
+        sum += a[i * k + t] * (float)qv * b_scales[(t / gs) * n + j];
+      }
+      c[i * n + j] = sum;
+    }
+  }
+  return ORC_OK;
+}
+
+/* The same sums in f64 (each term a[i][t] * q * scale exact in f64). */
+int32_t orc_gemm_wq_f64(uint32_t bits, uint64_t m, uint64_t n, uint64_t k, const float *a,
+                        const int8_t *w_q, const float *b_scales, uint64_t group_size,
+                        double *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || w_q == NULL || b_scales == NULL || c == NULL)
+    return ORC_ERR_INVALID_ARG;
+  if (bits != 8u && bits != 4u) return ORC_ERR_UNSUPPORTED;
+  const uint64_t gs = (group_size == 0u || group_size > k) ? k : group_size;
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      double sum = 0.0;
+      for (uint64_t t = 0; t < k; ++t) {
+        const uint64_t flat = t * n + j;
+        const int32_t qv = bits == 4u ? nibble_at(w_q, flat) : (int32_t)w_q[flat];
+        sum += (double)a[i * k + t] * (double)qv * (double)b_scales[(t / gs) * n + j];
+      }
+      c[i * n + j] = sum;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ---------------------------------------------------------------------- */
 /* Textbook encoders (llama.cpp ggml-quants.c reference quantizers)         */
 /* ---------------------------------------------------------------------- */
 

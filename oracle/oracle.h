@@ -49,10 +49,25 @@
  *                         token it equals the reference's sequence-mode
  *                         graph restated with orc_attention_f32 over all
  *                         positions (last row, bit-exact).
+ *   orc_quant_* /         the reference's models/quantize.c built into
+ *   orc_quantize_v0_f32 / oracle/_ref (bit-exact on random data, every
+ *   orc_dequantize_v0_f32 group size kind, odd lengths), the reference's
+ *                         own cases (tests/test_quantize.c:37-117), and
+ *                         closed forms: the largest |x| of a group maps to
+ *                         +-qmax, the round trip is within half a step,
+ *                         zero groups give scale 0.
+ *   orc_gemm_wq_seq_f32   the reference's ref_ops.c built into oracle/_ref
+ *                         (bit-exact), one-hot activations returning a
+ *                         dequantized row exactly, and orc_gemm_wq_f64.
+ *   orc_gemm_wq_f64       brute-force sums of exact terms on tiny shapes.
  *   orc_q8_0_encode_ref / textbook llama.cpp encoders used to pin the
- *   orc_q4_0_encode_ref   product encoders; the reference has no encoder,
- *                         so these two are pinned only by round-trip
- *                         bounds and by brute-force optimality checks.
+ *   orc_q4_0_encode_ref   product encoders; the reference has no encoder.
+ *                         Parity unpinned: they are checked only by the
+ *                         round-trip bound (half a step plus the f16
+ *                         rounding of the scale), the code ranges, and
+ *                         hand cases whose codes follow from the
+ *                         definition (a block's largest |x| maps to the
+ *                         extreme code).
  */
 #ifndef PAI_ORACLE_H
 #define PAI_ORACLE_H
@@ -101,6 +116,25 @@ int32_t orc_opt_gemv_avx2_mt(uint64_t m, uint64_t k, const float *a,
                              const float *x, float *y, int threads);
 int32_t orc_opt_gemm_avx2(uint64_t m, uint64_t n, uint64_t k, const float *a,
                           const float *b, float *c);
+/* v0 per-group scheme (models/quantize.h:36-40). */
+typedef struct orc_quant_scheme {
+  uint8_t bit_width;
+  uint8_t is_signed;
+  uint16_t group_size;
+} orc_quant_scheme_t;
+int32_t orc_quant_group_size(const orc_quant_scheme_t *s, uint64_t n, uint64_t *out_gs);
+uint64_t orc_quant_num_groups(uint64_t n, const orc_quant_scheme_t *s);
+uint64_t orc_quant_value_bytes(uint64_t n, const orc_quant_scheme_t *s);
+int32_t orc_quantize_v0_f32(const float *src, uint64_t n, const orc_quant_scheme_t *s,
+                            int8_t *out_q, float *out_scales, uint64_t *out_groups);
+int32_t orc_dequantize_v0_f32(const int8_t *q, const float *scales, uint64_t n,
+                              const orc_quant_scheme_t *s, float *out);
+int32_t orc_gemm_wq_seq_f32(uint32_t bits, uint64_t m, uint64_t n, uint64_t k, const float *a,
+                            const int8_t *w_q, const float *b_scales, uint64_t group_size,
+                            float *c);
+int32_t orc_gemm_wq_f64(uint32_t bits, uint64_t m, uint64_t n, uint64_t k, const float *a,
+                        const int8_t *w_q, const float *b_scales, uint64_t group_size,
+                        double *c);
 int32_t orc_opt_gemm_w8_avx2(uint64_t m, uint64_t n, uint64_t k,
                              const float *a, const int8_t *w_q,
                              const float *b_scales, uint64_t group_size,

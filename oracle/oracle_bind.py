@@ -45,6 +45,15 @@ _ORACLE_SIGS = {
     "orc_attention_last_f32": (C.c_int32, [C.c_uint64] * 5 + [_vp] * 4),
     "orc_argmax_first": (C.c_uint32, [_vp, C.c_uint64]),
     "orc_llama_step": (C.c_int32, [_vp, C.c_uint32, C.c_uint32, _vp, _vp]),
+    "orc_quant_group_size": (C.c_int32, [_vp, C.c_uint64, _vp]),
+    "orc_quant_num_groups": (C.c_uint64, [C.c_uint64, _vp]),
+    "orc_quant_value_bytes": (C.c_uint64, [C.c_uint64, _vp]),
+    "orc_quantize_v0_f32": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp, _vp]),
+    "orc_dequantize_v0_f32": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp]),
+    "orc_gemm_wq_seq_f32": (C.c_int32, [C.c_uint32] + [C.c_uint64] * 3 + [_vp] * 3 +
+                            [C.c_uint64, _vp]),
+    "orc_gemm_wq_f64": (C.c_int32, [C.c_uint32] + [C.c_uint64] * 3 + [_vp] * 3 +
+                        [C.c_uint64, _vp]),
 }
 
 _REF_SIGS = {
@@ -64,6 +73,15 @@ _REF_SIGS = {
     "pai_opt_gemm_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3),
     "pai_opt_gemm_w8_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
     "pai_opt_backend_name": (C.c_char_p, []),
+    "pai_ref_gemm_w8_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    "pai_ref_gemm_w4_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    "pai_quant_scheme_check": (C.c_int32, [_vp]),
+    "pai_quant_num_groups": (C.c_uint64, [C.c_uint64, _vp]),
+    "pai_quant_value_bytes": (C.c_uint64, [C.c_uint64, _vp]),
+    "pai_quant_scale_bytes": (C.c_uint64, [C.c_uint64, _vp]),
+    "pai_quant_weights_bytes": (C.c_uint64, [C.c_uint64, _vp]),
+    "pai_quantize_f32": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp, _vp]),
+    "pai_dequantize_f32": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp]),
     "pai_op_registry_init": (C.c_int32, [_vp]),
     "pai_op_registry_builtin": (C.c_int32, [_vp]),
     "pai_op_registry_register": (C.c_int32, [_vp, _vp]),
@@ -153,6 +171,78 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     if st != 0:
         raise RuntimeError(f"orc_silu_mul_f32 status {st}")
     return h
+
+
+class QuantScheme(C.Structure):
+    """The v0 scheme record (models/quantize.h:36-40)."""
+    _fields_ = [("bit_width", C.c_uint8), ("is_signed", C.c_uint8), ("group_size", C.c_uint16)]
+
+
+def v0_value_bytes(n: int, bits: int) -> int:
+    return (n + 1) // 2 if bits == 4 else n
+
+
+def v0_num_groups(n: int, group_size: int) -> int:
+    gs = n if group_size == 0 else group_size
+    return -(-n // gs)
+
+
+def v0_quantize(x: np.ndarray, bits: int, group_size: int, lib=None):
+    """orc_quantize_v0_f32 (or the reference build's pai_quantize_f32 when
+    `lib` is ref()): packed codes (int8) and one f32 scale per group."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    sch = QuantScheme(bits, 1, group_size)
+    q = np.empty(v0_value_bytes(x.size, bits), np.int8)
+    sc = np.empty(v0_num_groups(x.size, group_size), np.float32)
+    ng = C.c_uint64(0)
+    fn = lib.pai_quantize_f32 if lib is not None else oracle().orc_quantize_v0_f32
+    _check(fn(_p(x), x.size, C.byref(sch), _p(q), _p(sc), C.byref(ng)), "v0 quantize")
+    assert ng.value == sc.size
+    return q, sc
+
+
+def v0_dequantize(q: np.ndarray, scales: np.ndarray, n: int, bits: int, group_size: int,
+                  lib=None) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    sch = QuantScheme(bits, 1, group_size)
+    out = np.empty(n, np.float32)
+    fn = lib.pai_dequantize_f32 if lib is not None else oracle().orc_dequantize_v0_f32
+    _check(fn(_p(q), _p(scales), n, C.byref(sch), _p(out)), "v0 dequantize")
+    return out
+
+
+def gemm_wq_seq(bits: int, a: np.ndarray, w_q: np.ndarray, scales: np.ndarray, n: int,
+                group_size: int, lib=None) -> np.ndarray:
+    """c = a . dequant(W) with W [K][N] codes (int8, or nibbles over the flat
+    index t*n+j) and scales [G][N]: the reference's sequential f32 sum
+    (orc_gemm_wq_seq_f32, or pai_ref_gemm_w8_f32 / _w4_f32 of the reference
+    build when `lib` is ref())."""
+    a = _f32(a)
+    m, k = a.shape
+    w_q = np.ascontiguousarray(w_q, dtype=np.int8)
+    scales = _f32(scales)
+    c = np.empty((m, n), np.float32)
+    if lib is not None:
+        fn = lib.pai_ref_gemm_w8_f32 if bits == 8 else lib.pai_ref_gemm_w4_f32
+        st = fn(m, n, k, _p(a), _p(w_q), _p(scales), group_size, _p(c))
+    else:
+        st = oracle().orc_gemm_wq_seq_f32(bits, m, n, k, _p(a), _p(w_q), _p(scales), group_size,
+                                          _p(c))
+    _check(st, "gemm_wq_seq")
+    return c
+
+
+def gemm_wq_f64(bits: int, a: np.ndarray, w_q: np.ndarray, scales: np.ndarray, n: int,
+                group_size: int) -> np.ndarray:
+    a = _f32(a)
+    m, k = a.shape
+    w_q = np.ascontiguousarray(w_q, dtype=np.int8)
+    scales = _f32(scales)
+    c = np.empty((m, n), np.float64)
+    _check(oracle().orc_gemm_wq_f64(bits, m, n, k, _p(a), _p(w_q), _p(scales), group_size, _p(c)),
+           "gemm_wq_f64")
+    return c
 
 
 def _f32(a) -> np.ndarray:

@@ -49,6 +49,31 @@ def test_q8_0_q4_0_match_textbook_encoders(qtype, encode):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_textbook_encoders_hand_cases(sign):
+    """Codes fixed by the definitions: Q8_0 scales a block by d = amax/127
+    (f16), so its largest |x| takes code +-127; Q4_0 uses d = max/-8 with
+    max the signed value of largest magnitude, which takes code 0 and
+    dequantizes back to itself exactly when it is a power of two."""
+    o = ob.oracle()
+    x = np.full(32, 0.25 * sign, np.float32)
+    x[3] = 1.0 * sign
+    x[7] = 0.0
+    q8 = np.empty(34, np.uint8)
+    o.orc_q8_0_encode_ref(x.ctypes.data, q8.ctypes.data, 32)
+    d = np.frombuffer(q8[:2].tobytes(), np.float16)[0]
+    assert d == np.float16(np.float32(1.0) / np.float32(127.0))
+    codes = q8[2:].view(np.int8)
+    assert codes[3] == 127 * sign and codes[7] == 0
+    q4 = np.empty(18, np.uint8)
+    o.orc_q4_0_encode_ref(x.ctypes.data, q4.ctypes.data, 32)
+    d4 = np.frombuffer(q4[:2].tobytes(), np.float16)[0]
+    assert d4 == np.float16(-sign / 8.0)
+    assert q4[2 + 3] & 0x0F == 0              # element 3 (low nibble of byte 3): code 0
+    assert (q4[2 + 7] & 0x0F) == 8            # zero -> code 8
+    assert ob.dequant(2, q4, 32)[3] == np.float32(sign)
+
+
 def _bounds_check(qtype, w, blocks):
     qk = pa.BLOCK_ELEMS[qtype]
     deq = ob.dequant(qtype, blocks, w.size).reshape(w.shape)
