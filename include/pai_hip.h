@@ -88,6 +88,7 @@ const char *pai_hip_last_error(void);
 #define PAI_TUNE_GEMV_NO_MX 7u         /* 1: no matrix-core GEMV for 2..8 tokens */
 #define PAI_TUNE_MFMA_MIN_M 8u         /* tokens from which the MFMA GEMM runs */
 #define PAI_TUNE_GEMM_TILE 9u          /* 16-bit GEMM token tile: 1, 2, 3 = 32, 128, 256 */
+#define PAI_TUNE_V0_SEQUENTIAL 10u     /* 1: v0 GEMMs one thread per output  */
 pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value);
 
 /* Bytes occupied by `numel` elements of `type`; 0 when numel is not a
@@ -332,6 +333,97 @@ pai_status_t pai_qgemm_ref_f32(uint32_t type, uint64_t m, uint64_t n,
                                float *y);
 
 /* ---------------------------------------------------------------------- */
+/* v0 per-group formats (models/quantize.h)                                 */
+/* ---------------------------------------------------------------------- */
+
+/* Same field order, types and size as pai_quant_scheme_t
+ * (models/quantize.h:36-40): bit_width 4 or 8, is_signed 1, group_size 0
+ * for one group over the whole array. */
+typedef struct pai_hip_quant_scheme {
+  uint8_t bit_width;
+  uint8_t is_signed;
+  uint16_t group_size;
+} pai_hip_quant_scheme_t;
+
+/* c[m][n] = a[m][k] * W, W[k][n] stored as the reference's quantized-GEMM
+ * operands (cpu/reference/ref_ops.h:154-183): w_q int8 codes at t*n+j
+ * (w8), or two 4-bit codes per byte over that flat index (w4: low nibble
+ * for even indices, sign-extended), with one f32 scale per (group of
+ * group_size rows, column) at b_scales[(t/group_size)*n + j]; group_size 0
+ * or > k is one group over k. Same signatures and error codes as
+ * pai_ref_gemm_w8_f32 / pai_ref_gemm_w4_f32 (ref_ops.c:446-499), which
+ * they replace; host pointers, synchronous (the operands are copied to the
+ * device and back on every call, so they suit a registry dispatch with
+ * host buffers; resident weights use pai_hip_gemm_wq_f32_async).
+ * Results are within the f32 tolerance of the reference's sequential sum
+ * (rel-L2 1e-5 and below); shapes whose n is not a multiple of 16, or
+ * whose group_size is neither a multiple of 16 nor >= k, take a kernel
+ * that reproduces the reference's sum bit for bit. Dimensions up to
+ * 2^31 - 1 (UNSUPPORTED above). */
+pai_status_t pai_hip_gemm_w8_f32(uint64_t m, uint64_t n, uint64_t k,
+                                 const float *a, const int8_t *w_q,
+                                 const float *b_scales, uint64_t group_size,
+                                 float *c);
+pai_status_t pai_hip_gemm_w4_f32(uint64_t m, uint64_t n, uint64_t k,
+                                 const float *a, const int8_t *w_q4,
+                                 const float *b_scales, uint64_t group_size,
+                                 float *c);
+
+/* The same product on device pointers, enqueued on `stream` (a
+ * hipStream_t; NULL = default stream); bits 8 or 4. `workspace` (device
+ * memory, may be NULL) holds the split-K parts of small-M calls, which
+ * are summed in a fixed order by a second launch, so results repeat bit
+ * for bit; PAI_HIP_WQ_WORKSPACE_BYTES is enough for every shape, and a
+ * smaller or NULL workspace only reduces the split. Nothing is allocated.
+ * Calls sharing a workspace must not overlap. */
+#define PAI_HIP_WQ_WORKSPACE_BYTES (4u << 20)
+pai_status_t pai_hip_gemm_wq_f32_async(uint32_t bits, uint64_t m, uint64_t n,
+                                       uint64_t k, const float *a,
+                                       const void *w_q, const float *b_scales,
+                                       uint64_t group_size, float *c,
+                                       void *workspace,
+                                       uint64_t workspace_bytes, void *stream);
+
+/* models/quantize.h:63-75 on the GPU, bit for bit: per group
+ * scale = max|x| / qmax (127 or 7; NaN elements do not count),
+ * q = lrintf(x / scale) clamped to +-qmax (0 for a zero scale), 4-bit
+ * codes two per byte with element 2i in the low nibble (an odd tail's
+ * high nibble 0); out = scale * q. Same signatures and errors as
+ * pai_quantize_f32 / pai_dequantize_f32 (models/quantize.c:74-181): host
+ * pointers, synchronous. n up to 2^31 - 1 (UNSUPPORTED above). */
+pai_status_t pai_hip_quantize_f32(const float *src, uint64_t n,
+                                  const pai_hip_quant_scheme_t *scheme,
+                                  int8_t *out_q, float *out_scales,
+                                  uint64_t *out_num_groups);
+pai_status_t pai_hip_dequantize_f32(const int8_t *q, const float *scales,
+                                    uint64_t n,
+                                    const pai_hip_quant_scheme_t *scheme,
+                                    float *out);
+/* Device-pointer forms on `stream`: out_q and out 16-byte aligned. The
+ * session's load of a v0 tensor (models/model.c:264-290) maps to one
+ * pai_hip_dequantize_f32_async into the device region. */
+pai_status_t pai_hip_quantize_f32_async(const float *src, uint64_t n,
+                                        const pai_hip_quant_scheme_t *scheme,
+                                        int8_t *out_q, float *out_scales,
+                                        uint64_t *out_num_groups, void *stream);
+pai_status_t pai_hip_dequantize_f32_async(const int8_t *q, const float *scales,
+                                          uint64_t n,
+                                          const pai_hip_quant_scheme_t *scheme,
+                                          float *out, void *stream);
+
+/* CPU twins of pai_ref_gemm_w8_f32 / pai_ref_gemm_w4_f32 (the same
+ * signatures and results, bit for bit): the ref_fn of the qgemm_w8_f32 /
+ * qgemm_w4_f32 descriptors. They allocate nothing. */
+pai_status_t pai_gemm_w8_ref_f32(uint64_t m, uint64_t n, uint64_t k,
+                                 const float *a, const int8_t *w_q,
+                                 const float *b_scales, uint64_t group_size,
+                                 float *c);
+pai_status_t pai_gemm_w4_ref_f32(uint64_t m, uint64_t n, uint64_t k,
+                                 const float *a, const int8_t *w_q4,
+                                 const float *b_scales, uint64_t group_size,
+                                 float *c);
+
+/* ---------------------------------------------------------------------- */
 /* IR quantization tag of GGUF block weights                                */
 /* ---------------------------------------------------------------------- */
 
@@ -394,11 +486,14 @@ typedef struct pai_hip_op_descriptor {
   uint32_t reserved[2];
 } pai_hip_op_descriptor_t;
 
-/* The four descriptors "qgemm_q4_0_f32", "qgemm_q8_0_f32",
- * "qgemm_q4_k_f32", "qgemm_q6_k_f32" (inputs: x f32, packed weight u8;
- * output y f32; caps PAI_OP_CAP_CPU_REF | PAI_OP_CAP_GPU_HIP; ref_fn
- * pai_qgemm_ref_f32, which the dispatch site casts to that prototype, as
- * it casts the builtins' ref_fn to theirs; kernel_id PAI_KERNEL_NONE). The
+/* Six descriptors. "qgemm_q4_0_f32", "qgemm_q8_0_f32", "qgemm_q4_k_f32",
+ * "qgemm_q6_k_f32": inputs x f32 and the packed weight, output y f32,
+ * ref_fn pai_qgemm_ref_f32. "qgemm_w8_f32", "qgemm_w4_f32": inputs a,
+ * w_q, b_scales as the builtin gemm_w8_f32 / gemm_w4_f32
+ * (runtime/op_registry.c:268-285), ref_fn pai_gemm_w8_ref_f32 /
+ * pai_gemm_w4_ref_f32. All carry caps PAI_OP_CAP_CPU_REF |
+ * PAI_OP_CAP_GPU_HIP and kernel_id PAI_KERNEL_NONE; the dispatch site
+ * casts ref_fn to the prototype, as it casts the builtins' ref_fn. The
  * array is static and outlives any registry it is registered into. */
 const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count);
 

@@ -55,6 +55,16 @@ SIGNATURES = {
     "pai_qmat_upload_gguf": (C.c_int32, [C.POINTER(C.c_void_p), _vp, C.c_char_p]),
     "pai_qgemm_ref_f32": (C.c_int32, [C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, _vp, _vp,
                                       _vp]),
+    "pai_hip_gemm_w8_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    "pai_hip_gemm_w4_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    "pai_hip_gemm_wq_f32_async": (C.c_int32, [C.c_uint32] + [C.c_uint64] * 3 + [_vp] * 3 +
+                                  [C.c_uint64, _vp, _vp, C.c_uint64, _vp]),
+    "pai_hip_quantize_f32": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp, _vp]),
+    "pai_hip_dequantize_f32": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp]),
+    "pai_hip_quantize_f32_async": (C.c_int32, [_vp, C.c_uint64, _vp, _vp, _vp, _vp, _vp]),
+    "pai_hip_dequantize_f32_async": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp, _vp]),
+    "pai_gemm_w8_ref_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    "pai_gemm_w4_ref_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
     "pai_hip_quant_tag": (C.c_int32, [C.c_uint32, _vp]),
     "pai_hip_quant_type": (C.c_uint32, [_vp]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),

@@ -23,9 +23,9 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c", "pai_qref.c"]
+C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c", "pai_qref.c", "pai_v0.c"]
 HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemv_mx.hip", "qgemm.hip", "qdecode.hip",
-               "qscratch.hip"]
+               "qscratch.hip", "qv0.hip"]
 # qgemm.hip is also compiled once per block format (object name, defines):
 # the four formats' GEMM kernels build in parallel
 HIP_VARIANTS = [(f"qgemm_{f.lower()}.hip", "qgemm.hip",
@@ -67,7 +67,7 @@ def _compile(item) -> Path:
 def units() -> list:
     """Every compilation unit, longest first (so the pool starts them early)."""
     return [*HIP_VARIANTS, "qgemv.hip", "qgemv_mx.hip", "qlayout.hip", "qgemm.hip", "qdecode.hip",
-            "qscratch.hip", *C_SOURCES]
+            "qscratch.hip", "qv0.hip", *C_SOURCES]
 
 
 def build_library(jobs: int = 6) -> Path:

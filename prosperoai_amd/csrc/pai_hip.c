@@ -80,6 +80,7 @@ pai_status_t pai_hip_set_tuning(uint32_t knob, int32_t value) {
   case PAI_TUNE_GEMV_NO_MX: f = &paik_tune.gemv_no_mx; break;
   case PAI_TUNE_MFMA_MIN_M: f = &paik_tune.mfma_min_m; break;
   case PAI_TUNE_GEMM_TILE: f = &paik_tune.gemm_tile; break;
+  case PAI_TUNE_V0_SEQUENTIAL: f = &paik_tune.v0_sequential; break;
   default: return fail(PAI_ERR_INVALID_ARG, "unknown tuning knob %u", knob);
   }
   if (value < 0) return fail(PAI_ERR_INVALID_ARG, "tuning value %d < 0", (int)value);
@@ -743,6 +744,10 @@ static const pai_hip_op_descriptor_t k_ops[] = {
     {"qgemm_q8_0_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
     {"qgemm_q4_k_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
     {"qgemm_q6_k_f32", 1u, 2u, 1u, 0, 0, PAI_QGEMM_CAPS, PAI_QGEMM_REF, 0, {0u, 0u}},
+    {"qgemm_w8_f32", 1u, 3u, 1u, 0, 0, PAI_QGEMM_CAPS, (pai_status_t(*)(void))pai_gemm_w8_ref_f32,
+     0, {0u, 0u}},
+    {"qgemm_w4_f32", 1u, 3u, 1u, 0, 0, PAI_QGEMM_CAPS, (pai_status_t(*)(void))pai_gemm_w4_ref_f32,
+     0, {0u, 0u}},
 };
 
 const pai_hip_op_descriptor_t *pai_hip_op_descriptors(uint32_t *count) {

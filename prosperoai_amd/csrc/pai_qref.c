@@ -12,6 +12,9 @@
  * its results equal that composition bit for bit. The dequantization runs
  * one block at a time into a stack buffer and the sums accumulate in y, so
  * nothing is allocated. Built without floating-point contraction.
+ *
+ * The twins of the v0 GEMMs (pai_ref_gemm_w8_f32 / _w4_f32,
+ * cpu/reference/ref_ops.c:446-499) follow at the end.
  */
 #include <stdint.h>
 #include <string.h>
@@ -141,4 +144,44 @@ pai_status_t pai_qgemm_ref_f32(uint32_t type, uint64_t m, uint64_t n, uint64_t k
     }
   }
   return PAI_OK;
+}
+
+/* Code (t, j) of a [K][N] operand: int8, or the sign-extended nibble at
+ * flat index t*n+j (low nibble for even indices). */
+static int32_t wq_code(uint32_t bits, const int8_t *w, uint64_t flat) {
+  if (bits == 8u) return w[flat];
+  const uint8_t byte = (uint8_t)w[flat / 2u];
+  const int32_t nib = (flat & 1u) == 0u ? (byte & 0x0F) : (byte >> 4);
+  return (nib & 0x08) ? nib - 16 : nib;
+}
+
+/* c[i][j] = sum over t ascending of (a[i][t] * q(t, j)) * scale, the
+ * reference's order and roundings. */
+static pai_status_t gemm_wq_ref(uint32_t bits, uint64_t m, uint64_t n, uint64_t k, const float *a,
+                                const int8_t *w, const float *b_scales, uint64_t group_size,
+                                float *c) {
+  if (m == 0u || n == 0u || k == 0u || a == NULL || w == NULL || b_scales == NULL || c == NULL)
+    return PAI_ERR_INVALID_ARG;
+  const uint64_t gs = (group_size == 0u || group_size > k) ? k : group_size;
+  for (uint64_t i = 0; i < m; ++i) {
+    for (uint64_t j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (uint64_t t = 0; t < k; ++t)
+        sum += a[i * k + t] * (float)wq_code(bits, w, t * n + j) * b_scales[(t / gs) * n + j];
+      c[i * n + j] = sum;
+    }
+  }
+  return PAI_OK;
+}
+
+pai_status_t pai_gemm_w8_ref_f32(uint64_t m, uint64_t n, uint64_t k, const float *a,
+                                 const int8_t *w_q, const float *b_scales, uint64_t group_size,
+                                 float *c) {
+  return gemm_wq_ref(8u, m, n, k, a, w_q, b_scales, group_size, c);
+}
+
+pai_status_t pai_gemm_w4_ref_f32(uint64_t m, uint64_t n, uint64_t k, const float *a,
+                                 const int8_t *w_q4, const float *b_scales, uint64_t group_size,
+                                 float *c) {
+  return gemm_wq_ref(4u, m, n, k, a, w_q4, b_scales, group_size, c);
 }

@@ -62,6 +62,7 @@ typedef struct paik_tune {
   int32_t gemv_no_mx;         /* 1: 2..8-token calls stay on the integer-dot GEMV */
   int32_t mfma_min_m;         /* tokens from which calls take the MFMA GEMM (0: 8) */
   int32_t gemm_tile;          /* 16-bit GEMM tile: 1 = 32 tokens, 2 = 128, 3 = 256 (0: by M) */
+  int32_t v0_sequential;      /* 1: v0 GEMMs on the one-thread-per-output kernel */
 } paik_tune_t;
 extern paik_tune_t paik_tune;
 
@@ -111,6 +112,28 @@ int paik_gemv_mx(const paik_qview_t *const *vs, float *const *ys,
                  uint32_t count, uint32_t m, const float *x, void *stream);
 int paik_gemv_mx_silu_mul(const paik_qview_t *gate, const paik_qview_t *up,
                           uint32_t m, const float *x, float *h, void *stream);
+
+/* v0 per-group formats (qv0.hip). */
+typedef struct paik_v0_gemm {
+  const float *a;          /* [m][k] f32                                     */
+  const void *wq;          /* [k][n] int8 codes, or nibbles over t*n+j        */
+  const float *scales;     /* [ceil(k/gs)][n]                                */
+  float *c;                /* [m][n]                                         */
+  void *workspace;         /* split-K parts (may be NULL: no split)           */
+  uint64_t workspace_bytes;
+  uint32_t bits, m, n, k;  /* m <= 65535 per launch                          */
+  uint32_t gs;             /* group rows, 1..k                               */
+  int strip_ok;            /* n % 16 == 0, gs % 16 == 0 or gs == k, wq and
+                              scales 16-byte aligned: the strip kernel runs   */
+  int sequential;          /* the one-thread-per-output kernel regardless     */
+} paik_v0_gemm_t;
+int paik_v0_gemm(const paik_v0_gemm_t *p, void *stream);
+/* n < 2^31; q 16-byte aligned; scales hold ceil(n/gs) floats */
+int paik_v0_quantize(const float *x, uint32_t n, uint32_t bits, uint32_t gs, int8_t *q,
+                     float *scales, void *stream);
+/* out 16-byte aligned */
+int paik_v0_dequantize(const int8_t *q, const float *scales, uint32_t n, uint32_t bits,
+                       uint32_t gs, float *out, void *stream);
 
 /* Decode-step kernels (qdecode.hip). kc/vc are fp16 caches [hk][ctx][hd]. */
 uint32_t paik_norm_max(void);

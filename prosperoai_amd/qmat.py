@@ -53,7 +53,8 @@ def init() -> None:
 
 # pai_hip_set_tuning knobs (include/pai_hip.h)
 TUNE = {"gemm_splits": 1, "gemm_no_x16": 2, "gemm_atomic_splits": 3, "gemv_wgs": 4,
-        "gemv_rows": 5, "gemv_nw": 6, "gemv_no_mx": 7, "mfma_min_m": 8, "gemm_tile": 9}
+        "gemv_rows": 5, "gemv_nw": 6, "gemv_no_mx": 7, "mfma_min_m": 8, "gemm_tile": 9,
+        "v0_sequential": 10}
 
 
 def set_tuning(name: str, value: int) -> None:

@@ -11,7 +11,9 @@
 
 #include <pai/op.h>
 
+#include "cpu/reference/ref_ops.h"
 #include "ir/ir.h"
+#include "models/quantize.h"
 #include "pai_hip.h"
 
 #define SAME_FIELD(A, B, f)                                                                    \
@@ -45,6 +47,17 @@ SAME_FIELD(pai_hip_ir_quant_t, pai_ir_quant_t, group_size);
 _Static_assert(PAI_IR_QUANT_BLOCK_GGUF == (unsigned)PAI_IR_QUANT_BLOCK_COUNT, "next value");
 _Static_assert(PAI_IR_QUANT_REPR_F16 == 1, "f16 repr value");
 
+/* v0 schemes and GEMMs: the same record and the same prototypes */
+_Static_assert(sizeof(pai_hip_quant_scheme_t) == sizeof(pai_quant_scheme_t), "scheme size");
+SAME_FIELD(pai_hip_quant_scheme_t, pai_quant_scheme_t, bit_width);
+SAME_FIELD(pai_hip_quant_scheme_t, pai_quant_scheme_t, is_signed);
+SAME_FIELD(pai_hip_quant_scheme_t, pai_quant_scheme_t, group_size);
+#define SAME_TYPE(a, b) _Static_assert(__builtin_types_compatible_p(__typeof__(&a), __typeof__(&b)), #a)
+SAME_TYPE(pai_hip_gemm_w8_f32, pai_ref_gemm_w8_f32);
+SAME_TYPE(pai_hip_gemm_w4_f32, pai_ref_gemm_w4_f32);
+SAME_TYPE(pai_gemm_w8_ref_f32, pai_ref_gemm_w8_f32);
+SAME_TYPE(pai_gemm_w4_ref_f32, pai_ref_gemm_w4_f32);
+
 /* What a GGUF-aware pai_kernel_select resolves a GEMM to: the weight's tag
  * picks the qgemm descriptor, an untagged weight keeps matmul_f32. */
 static const char *gemm_op_name(const pai_hip_ir_quant_t *weight_tag) {
@@ -71,6 +84,20 @@ int main(void) {
       return 6;
     if (op->ref_fn != (pai_op_ref_fn)pai_qgemm_ref_f32) return 7;
   }
+  /* the v0 GEMMs: three inputs as the builtin gemm_w8_f32 / gemm_w4_f32,
+   * whose entries stay in place */
+  const char *v0[2] = {"qgemm_w8_f32", "qgemm_w4_f32"};
+  const pai_op_ref_fn v0_ref[2] = {(pai_op_ref_fn)pai_gemm_w8_ref_f32,
+                                   (pai_op_ref_fn)pai_gemm_w4_ref_f32};
+  for (int i = 0; i < 2; ++i) {
+    const pai_op_descriptor_t *op = pai_op_registry_lookup(&reg, v0[i]);
+    if (op == NULL || op->num_inputs != 3u || op->ref_fn != v0_ref[i]) return 10;
+    if (!pai_op_supports(op, PAI_OP_CAP_CPU_REF) || !pai_op_supports(op, PAI_OP_CAP_GPU_HIP))
+      return 11;
+  }
+  if (pai_op_registry_lookup(&reg, "gemm_w8_f32") == NULL ||
+      pai_op_registry_lookup(&reg, "gemm_w4_f32") == NULL)
+    return 12;
   pai_hip_ir_quant_t plain;
   memset(&plain, 0, sizeof plain);
   if (strcmp(gemm_op_name(&plain), "matmul_f32") != 0) return 8;

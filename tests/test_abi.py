@@ -82,12 +82,16 @@ def test_argument_errors_before_device():
 def test_descriptors_layout_and_names():
     ds = pa.descriptors()
     assert [d.name.decode() for d in ds] == ["qgemm_q4_0_f32", "qgemm_q8_0_f32",
-                                             "qgemm_q4_k_f32", "qgemm_q6_k_f32"]
-    for d in ds:
-        assert d.caps == (1 << 0) | (1 << 3) and d.num_inputs == 2 and d.num_outputs == 1
-        # the CPU twin, pai_qgemm_ref_f32, is every descriptor's reference function
-        twin = C.cast(pa.lib().pai_qgemm_ref_f32, C.c_void_p).value
-        assert d.ref_fn == twin and d.kernel_id == 0 and d.in_dtype == 0
+                                             "qgemm_q4_k_f32", "qgemm_q6_k_f32",
+                                             "qgemm_w8_f32", "qgemm_w4_f32"]
+    twins = [pa.lib().pai_qgemm_ref_f32] * 4 + [pa.lib().pai_gemm_w8_ref_f32,
+                                                pa.lib().pai_gemm_w4_ref_f32]
+    for d, twin in zip(ds, twins):
+        assert d.caps == (1 << 0) | (1 << 3) and d.num_outputs == 1
+        assert d.num_inputs == (3 if d.name.startswith(b"qgemm_w") else 2)
+        # each descriptor's reference function is its CPU twin
+        assert d.ref_fn == C.cast(twin, C.c_void_p).value
+        assert d.kernel_id == 0 and d.in_dtype == 0
     # pai_op_descriptor_t is 56 bytes on LP64 (sdk/include/pai/op.h:71-82)
     assert C.sizeof(HipDescriptor) == 56
     assert HipDescriptor.ref_fn.offset == 32 and HipDescriptor.kernel_id.offset == 40
@@ -108,7 +112,8 @@ def test_descriptors_register_into_reference_registry(ref_lib):
     for i in range(count.value):
         assert ref_lib.pai_op_registry_register(reg, ptr + i * C.sizeof(HipDescriptor)) == 0
     assert ref_lib.pai_op_registry_count(reg) == base + count.value
-    for name in (b"qgemm_q4_0_f32", b"qgemm_q8_0_f32", b"qgemm_q4_k_f32", b"qgemm_q6_k_f32"):
+    for name in (b"qgemm_q4_0_f32", b"qgemm_q8_0_f32", b"qgemm_q4_k_f32", b"qgemm_q6_k_f32",
+                 b"qgemm_w8_f32", b"qgemm_w4_f32"):
         d = ref_lib.pai_op_registry_lookup(reg, name)
         assert d is not None
         assert ref_lib.pai_op_supports(d, 1 << 3) == 1

@@ -133,4 +133,56 @@ def test_c_program_against_reference_headers(ref_lib, tmp_path):
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
-    assert "boundary ok: 4 descriptors" in r.stdout
+    assert "boundary ok: 6 descriptors" in r.stdout
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("m,n,k,gs", [(3, 5, 8, 4), (2, 33, 70, 32), (1, 64, 128, 0), (4, 7, 9, 100)])
+def test_v0_cpu_twins_equal_reference_build(ref_lib, bits, m, n, k, gs):
+    """pai_gemm_w8_ref_f32 / _w4_ref_f32 against the reference build's
+    pai_ref_gemm_w8_f32 / _w4_f32, bit for bit."""
+    import oracle_bind as ob
+    rng = np.random.default_rng(m + n + k + bits)
+    nbytes = k * n if bits == 8 else (k * n + 1) // 2
+    w = rng.integers(-128, 128, nbytes).astype(np.int8)
+    sc = rng.uniform(0.001, 0.05, (-(-k // (gs if 0 < gs <= k else k)), n)).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    want = ob.gemm_wq_seq(bits, a, w, sc, n, gs, lib=ref_lib)
+    got = np.empty((m, n), np.float32)
+    fn = lib().pai_gemm_w8_ref_f32 if bits == 8 else lib().pai_gemm_w4_ref_f32
+    assert fn(m, n, k, a.ctypes.data, w.ctypes.data, sc.ctypes.data, gs, got.ctypes.data) == 0
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert fn(0, n, k, a.ctypes.data, w.ctypes.data, sc.ctypes.data, gs, got.ctypes.data) == -1
+    assert fn(m, n, k, None, w.ctypes.data, sc.ctypes.data, gs, got.ctypes.data) == -1
+
+
+def test_v0_entry_points_check_arguments_without_a_gpu():
+    """Argument errors come back before any device work (no GPU here)."""
+    L = lib()
+    a = np.zeros(4, np.float32)
+    w = np.zeros(4, np.int8)
+    for fn in (L.pai_hip_gemm_w8_f32, L.pai_hip_gemm_w4_f32):
+        assert fn(0, 1, 1, a.ctypes.data, w.ctypes.data, a.ctypes.data, 0, a.ctypes.data) == -1
+        assert fn(1, 1, 1, None, w.ctypes.data, a.ctypes.data, 0, a.ctypes.data) == -1
+    assert L.pai_hip_gemm_wq_f32_async(6, 1, 1, 1, a.ctypes.data, w.ctypes.data, a.ctypes.data,
+                                       0, a.ctypes.data, None, 0, None) == -3
+    bad = Scheme(16, 1, 0)
+    unsigned = Scheme(8, 0, 0)
+    assert L.pai_hip_quantize_f32(a.ctypes.data, 4, C.byref(bad), w.ctypes.data, a.ctypes.data,
+                                  None) == -3
+    assert L.pai_hip_quantize_f32(a.ctypes.data, 4, C.byref(unsigned), w.ctypes.data,
+                                  a.ctypes.data, None) == -3
+    assert L.pai_hip_quantize_f32(a.ctypes.data, 4, None, w.ctypes.data, a.ctypes.data,
+                                  None) == -1
+    assert L.pai_hip_quantize_f32(None, 4, C.byref(Scheme(8, 1, 0)), w.ctypes.data,
+                                  a.ctypes.data, None) == -1
+    # n == 0 with one group over the array: a zero group size (quantize.c:20-23)
+    assert L.pai_hip_quantize_f32(a.ctypes.data, 0, C.byref(Scheme(8, 1, 0)), w.ctypes.data,
+                                  a.ctypes.data, None) == -1
+    assert L.pai_hip_dequantize_f32(w.ctypes.data, None, 4, C.byref(Scheme(8, 1, 0)),
+                                    a.ctypes.data) == -1
+
+
+class Scheme(C.Structure):
+    """pai_hip_quant_scheme_t (the layout of the reference's pai_quant_scheme_t)."""
+    _fields_ = [("bit_width", C.c_uint8), ("is_signed", C.c_uint8), ("group_size", C.c_uint16)]
