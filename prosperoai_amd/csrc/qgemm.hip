@@ -1,25 +1,34 @@
 /*
  * Batched / prefill GEMM over packed blocks on MFMA (gfx950).
  *
- * y[M][N] = x[M][K] · Wᵀ: weights dequantized in registers to fp16 (or
- * bf16), activations rounded to the same type through LDS,
- * v_mfma_f32_16x16x32_{f16,bf16} with f32 accumulation.
+ * y[M][N] = x[M][K] · Wᵀ with v_mfma_f32_32x32x16_{f16,bf16} and f32
+ * accumulation: weights dequantized to fp16 (or bf16), activations
+ * rounded once to the same type. Operand layout of the 32x32x16 form:
+ * lane l supplies row l%32 of A and column l%32 of B, each with 8 K values
+ * (k-set l/32).
  *
- * Workgroup: 4 waves, 256 weight rows x TT tokens (TT = 128 or 32); each
- * wave owns 64 rows (four 16-row groups) and all TT tokens, so no weight
- * value is shared between waves and the weights never pass through LDS:
- * a lane fetches whole chunks straight into registers and turns them into
- * MFMA operands. A step covers 128 columns, i.e. four chunks per row.
+ * k_gemm_x16 / k_gemm (weights dequantized in registers). A workgroup owns
+ * RWG weight rows x TT tokens (256 x 32, 256 x 128 on 8 waves; 128 x 256
+ * on 4 waves); each wave owns RWG/NW rows as 32-row fragments and all TT
+ * tokens, so no weight value is shared between waves and the weights never
+ * pass through LDS: a lane fetches whole chunks into registers and turns
+ * them into MFMA operands. A step covers 128 columns (four chunks per
+ * row). Because every operand is already scaled, the two k-sets of one
+ * MFMA need not come from the same chunk: lane (r, g) (r = l%32, g = l/32)
+ * loads chunks 4s + 2u + g of row r (u = 0, 1), and MFMA (u, w) takes
+ * nibble word w of that chunk (its columns 8w..8w+7) as the k-set, so one
+ * 16-byte load feeds four MFMAs. Activations come from the 16-bit copy
+ * k_cvt_x made (k_gemm_x16: staged into LDS by buffer_load ... lds DMA) or
+ * from f32 x rounded through registers (k_gemm, without a workspace).
  *
- * Operand layout of v_mfma_f32_16x16x32_*: lane l supplies row l%16 of A
- * and column l%16 of B, each with 8 K values ("k-set" l/16); D[4(l/16)+i]
- * [l%16] lands in lane l. Because every operand is already scaled, the
- * four k-sets of one MFMA need not come from the same chunk: lane (r, g)
- * (r = l%16, g = l/16) loads chunk 4s+g of row r, and MFMA number w of the
- * step (w = 0..3) takes nibble word w of that chunk (its columns
- * 8w..8w+7) as the k-set. The B lane (t, g) reads the matching 8
- * activations x[t][128s + 32g + 8w ..] from LDS. One 16-byte load per lane
- * thus covers 4 chunks of 16 rows (64 contiguous bytes of each row).
+ * k_gemm_lds (weights dequantized once per workgroup into LDS). A
+ * workgroup owns 128 weight rows x 256 tokens on 8 waves; per 64-column
+ * stage each thread dequantizes 16 columns of one row into the 16 KiB
+ * weight tile (double-buffered) while the 32 KiB activation tile of a
+ * later stage arrives by DMA (4 buffers), and every wave reads both MFMA
+ * operands from LDS. Its weight loads are asm with waits written against
+ * the registers they fill, with exact counts (the compiler cannot count
+ * the asm DMA, and would otherwise wait for everything).
  *
  * Dequantization to 16 bits costs about two VALU operations per weight:
  * the 4-bit (or 6- and 8-bit) codes are gathered into bytes, v_perm_b32
@@ -29,11 +38,11 @@
  * value = s * q' + b equals the reference's f32 value to within one f32
  * rounding of b, far below the fp16 rounding that follows.
  *
- * Per step a wave issues 4 x (TT/16) x 4 MFMAs; the dequantization of the
- * next step's operands (loaded a full step earlier) and the conversion of
- * the next activation tile into the other LDS buffer are interleaved with
- * them. Shapes with few tiles split K across workgroups whose partial sums
- * are added into y (zeroed first) with f32 atomics.
+ * Shapes with few tiles split K across workgroups: single-matrix launches
+ * add their partial tiles into y (zeroed first) with f32 atomics, so with
+ * more than two parts the last bits depend on the order of the adds;
+ * multi-matrix launches store the parts in a workspace and sum them in a
+ * fixed order (k_split_reduce).
  *
  * Workgroups are numbered so that the ones resident on one XCD (hardware
  * places workgroup i on XCD i % 8) take consecutive tiles of one token
