@@ -1,15 +1,15 @@
 #!/usr/bin/env python3
 """Quantized-weights GEMV/GEMM benchmark on one MI355X.
 
-Headline (the JSON `value`): Q4_0 decode GEMV, M=1, over the seven
-Llama-3-8B per-layer projections (q, o: 4096x4096; k, v: 1024x4096;
+Headline (the JSON `value`): Q4_K decode GEMV, M=1 (the north-star
+format), over the seven Llama-3-8B per-layer projections (q, o: 4096x4096; k, v: 1024x4096;
 gate, up: 14336x4096; down: 4096x14336), issued as one layer's decode step:
 q/k/v in one fused call (they share the attention input), o, gate/up in one
 fused call (they share the FFN input), down -- four launches streaming the
 seven matrices. Steps rotate over --layers distinct weight copies so the
 working set (123 MB per layer) exceeds the 256 MB Infinity Cache. Weights
-are f32 N(0, 0.02^2) from a fixed seed, quantized by libpai_hip's encoder;
-activations are f32 N(0, 1), resident in HBM.
+are f32 N(0, 0.02^2) from a fixed seed, quantized by libpai_hip's K-quant
+encoder; activations are f32 N(0, 1), resident in HBM.
 
 value    = algorithmic bytes (packed W + x + y, f32) of all timed steps
            / wall time between two stream synchronisations.
@@ -20,9 +20,9 @@ cpu_baseline = the reference's AVX2+FMA GEMV (cpu/optimized/opt_ops.c,
            compiled from its sources into oracle/_ref; this repository's
            restatement when that build is absent) on the dequantized f32
            weights of the same seven projections, one host core.
-extra    = the seven projections as separate launches; the step with
-           silu(gate)*up fused into the gate/up launch; Q4_K at M in
-           {1, 8, 32}; Q8_0 4096x4096 GEMV; and the M=512 prefill GEMMs
+extra    = the same step in Q4_0 (fused, as seven separate launches, and
+           with silu(gate)*up fused into the gate/up launch); Q4_K at M in
+           {8, 32}; Q8_0 4096x4096 GEMV; and the M=512 prefill GEMMs
            (gate Q4_K, down Q6_K, and gate+up with the fused silu*mul) in
            TFLOP/s against 2.5 PFLOP/s dense fp16; and the full decode step
            of a Llama-3-8B-shape model with an fp16 KV cache at context
@@ -48,6 +48,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 PROJ = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
         ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 METRIC = "quant GEMV GB/s (%HBM peak) at 8B shapes; M=512 GEMM TFLOPS"
+HEAD_QTYPE, HEAD_CONFIG = 12, 3  # Q4_K, the third configuration (M in {1, 8, 32}) at M = 1
+HEAD_NAME = "Q4_K"
 
 
 def log(msg: str) -> None:
@@ -244,12 +246,12 @@ def q8_config1(pa, hm, steps: int) -> dict:
 
 
 def host_pointer_step(pa, reps: int = 50) -> dict:
-    """The seven Q4_0 projections through the synchronous host-pointer
+    """The seven headline-format projections through the synchronous host-pointer
     entry point (pai_qgemm_f32 without PAI_QGEMM_DEVICE_PTRS: x is copied
     to the device and y back over PCIe on every call), wall clock per
     step. Reported beside the HBM-resident figure, never as the value."""
-    blocks = quantized_layer(pa, pa.Q4_0, 2)
-    layer = Layer(pa, pa.Q4_0, blocks)
+    blocks = quantized_layer(pa, HEAD_QTYPE, HEAD_CONFIG)
+    layer = Layer(pa, HEAD_QTYPE, blocks)
     kmax = max(k for _, _, k in PROJ)
     x = pa.normal_f32(0xC0DE0000 ^ 0x5A5A, kmax)
     xs = [x[:k] for _, _, k in PROJ]
@@ -264,7 +266,7 @@ def host_pointer_step(pa, reps: int = 50) -> dict:
     for w in layer.w:
         w.free()
     med = float(np.median(times))
-    b = sum(call_bytes(pa, pa.Q4_0, n, k) for _, n, k in PROJ)
+    b = sum(call_bytes(pa, HEAD_QTYPE, n, k) for _, n, k in PROJ)
     return {"us_per_step": round(med * 1e6, 1), "GBps": round(b / med / 1e9, 1),
             "calls_per_step": len(PROJ)}
 
@@ -418,18 +420,18 @@ def decode_8b(pa, hm, steps: int, warmup: int, fill: int = 2048, threads: int = 
 
 def cpu_baseline(pa, budget_s: float) -> dict:
     """The reference's single-thread AVX2 GEMV on dequantized f32 weights of
-    the seven Q4_0 projections (bounded number of passes)."""
+    the seven headline-format projections (bounded number of passes)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle_bind as ob
     r = ob.ref()
     kind = "reference" if r is not None else "port"
-    blocks = quantized_layer(pa, pa.Q4_0, 2)
+    blocks = quantized_layer(pa, HEAD_QTYPE, HEAD_CONFIG)
     mats = []
     for (_, n, k), b in zip(PROJ, blocks):
         if r is not None:
-            mats.append(ob.ref_dequant(pa.Q4_0, b.tobytes(), n * k, row=k).reshape(n, k))
+            mats.append(ob.ref_dequant(HEAD_QTYPE, b.tobytes(), n * k, row=k).reshape(n, k))
         else:
-            mats.append(ob.dequant(pa.Q4_0, b, n * k).reshape(n, k))
+            mats.append(ob.dequant(HEAD_QTYPE, b, n * k).reshape(n, k))
     kmax = max(k for _, _, k in PROJ)
     x = pa.normal_f32(0xC0DE0000 ^ 0x5A5A, kmax)
     ys = [np.empty(n, np.float32) for _, n, _ in PROJ]
@@ -449,7 +451,7 @@ def cpu_baseline(pa, budget_s: float) -> dict:
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > budget_s and len(times) >= 3:
             break
-    bytes_step = sum(call_bytes(pa, pa.Q4_0, n, k) for _, n, k in PROJ)
+    bytes_step = sum(call_bytes(pa, HEAD_QTYPE, n, k) for _, n, k in PROJ)
     med = float(np.median(times))
 
     def timed(fn, budget: float, least: int = 3) -> list:
@@ -498,7 +500,7 @@ def cpu_baseline(pa, budget_s: float) -> dict:
                                            f"(the AVX2 row kernel, rows split over {threads} "
                                            f"threads)"},
             "w8_gemm_q8_0_shape": w8,
-            "sample": f"{len(times)} passes over the seven Q4_0 projections of one layer "
+            "sample": f"{len(times)} passes over the seven {HEAD_NAME} projections of one layer "
                       f"(pai_opt_gemv_f32 on dequantized f32 [N][K], 4 B/weight touched); "
                       f"median {med * 1e3:.1f} ms/pass, min {min(times) * 1e3:.1f} ms; "
                       f"GB/s counts the same packed bytes as the GPU value",
@@ -600,17 +602,19 @@ def kernel_pmc_summary(paths: list) -> dict:
 
 def trace_summary(trace_csv: str, steps: int, warmup: int, layers: int) -> dict:
     """Kernel durations of the headline's timed region from a rocprofv3
-    --kernel-trace CSV of a default run: the first Q4_0 GEMV dispatches are
+    --kernel-trace CSV of a default run: the first headline GEMV dispatches are
     the eager pass over the layers and the warm-up graph replays, then come
     the timed steps (4 launches each, in step order qkv, o, gate_up, down)."""
     import csv
-    rows = [r for r in csv.DictReader(open(trace_csv)) if "k_gemv<paik::Q4_0" in r["Kernel_Name"]]
+    rows = [r for r in csv.DictReader(open(trace_csv))
+            if f"k_gemv<paik::{HEAD_NAME}" in r["Kernel_Name"]]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     nl = len(FUSED_STEP)
     skip = nl * layers + nl * layers * max(1, -(-warmup // layers))
     timed = rows[skip:skip + nl * steps]
     if len(timed) != nl * steps:
-        raise RuntimeError(f"{trace_csv}: {len(rows)} Q4_0 GEMV dispatches, expected {skip} + {nl * steps}")
+        raise RuntimeError(f"{trace_csv}: {len(rows)} {HEAD_NAME} GEMV dispatches, "
+                           f"expected {skip} + {nl * steps}")
     dur = np.array([int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in timed], float)
     out = {"dispatches": len(timed), "skipped": skip,
            "mean_ns": round(float(dur.mean()), 1),
@@ -657,7 +661,7 @@ def main() -> int:
     ap.add_argument("--kernel-pmc-summary", nargs="+", metavar="PMC_CSV",
                     help="per-kernel durations and counter means of rocprofv3 --pmc CSVs, "
                          "then exit")
-    ap.add_argument("--pmc-kernel", default="k_gemv<paik::Q4_0",
+    ap.add_argument("--pmc-kernel", default=f"k_gemv<paik::{HEAD_NAME}",
                     help="kernel-name substring for --pmc-summary")
     ap.add_argument("--trace-summary", metavar="TRACE_CSV",
                     help="summarise the headline's timed-region GEMV dispatches of a "
@@ -694,20 +698,20 @@ def main() -> int:
         if args.calib_copy_mib:
             copy_calibration(hm, args.calib_copy_mib)
         return 0
-    log(f"Q4_0 M=1 x {args.layers} layers")
+    log(f"{HEAD_NAME} M=1 x {args.layers} layers")
 
-    head = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, args.steps, args.warmup,
+    head = gemv_config(pa, hm, HEAD_QTYPE, HEAD_CONFIG, 1, args.layers, args.steps, args.warmup,
                        launch_detail=not args.no_launch_detail)
-    log(f"Q4_0 M=1 fused step: {head['GBps']:.1f} GB/s wall, {head['gpu_GBps']:.1f} GB/s GPU; "
+    log(f"{HEAD_NAME} M=1 fused step: {head['GBps']:.1f} GB/s wall, {head['gpu_GBps']:.1f} GB/s GPU; "
         f"{head.get('per_launch')}")
     avg_us = head["gpu_ms_per_step"] * 1e3 / head["launches_per_step"]
     roof = {"bound": "hbm", "achieved": round(head["gpu_GBps"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(head["gpu_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None, "kernel": "paik::k_gemv<paik::Q4_0, U, 1, false, NW>",
+            "traffic": None, "kernel": f"paik::k_gemv<paik::{HEAD_NAME}, U, 1, false, NW>",
             "launches_per_step": head["launches_per_step"],
             "bytes_per_launch": round(head["bytes_per_step"] / head["launches_per_step"]),
             "avg_launch_us": round(avg_us, 3)}
-    traffic_file = ROOT / "profiles" / "traffic_gemv_q4_0_decode_step.txt"
+    traffic_file = ROOT / "profiles" / f"traffic_gemv_{HEAD_NAME.lower()}_decode_step.txt"
     if traffic_file.exists():  # measured by two counter runs of this script (see the file)
         for ln in traffic_file.read_text().splitlines():
             if ln.startswith("traffic_bytes_per_launch:"):
@@ -716,6 +720,9 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         try:
+            extra["q4_0_m1"] = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, 300, 20)
+            log(f"Q4_0 M=1: {extra['q4_0_m1']['gpu_GBps']:.1f} GB/s GPU; "
+                f"{extra['q4_0_m1']['per_launch']}")
             extra["q4_0_m1_separate"] = gemv_config(pa, hm, pa.Q4_0, 2, 1, args.layers, 300, 20,
                                                     plan=SEPARATE_STEP)
             log(f"Q4_0 M=1 separate: {extra['q4_0_m1_separate']['gpu_GBps']:.1f} GB/s GPU")
@@ -724,15 +731,12 @@ def main() -> int:
             log(f"Q4_0 M=1 with silu*mul fused: "
                 f"{extra['q4_0_m1_silu_fused']['gpu_GBps']:.1f} GB/s GPU; "
                 f"{extra['q4_0_m1_silu_fused']['per_launch']}")
-            extra["q4_k_m1"] = gemv_config(pa, hm, pa.Q4_K, 3, 1, args.layers, 300, 20)
-            log(f"Q4_K M=1: {extra['q4_k_m1']['gpu_GBps']:.1f} GB/s GPU; "
-                f"{extra['q4_k_m1']['per_launch']}")
             for m in (8, 32):
                 extra[f"q4_k_m{m}"] = gemv_config(pa, hm, pa.Q4_K, 3, m, args.layers, 100, 5)
                 log(f"Q4_K M={m}: {extra[f'q4_k_m{m}']['gpu_GBps']:.1f} GB/s GPU")
             extra["q8_0_4096x4096_m1"] = q8_config1(pa, hm, 300)
-            extra["q4_0_m1_host_pointers"] = host_pointer_step(pa)
-            log(f"Q4_0 M=1 host pointers: {extra['q4_0_m1_host_pointers']}")
+            extra["q4_k_m1_host_pointers"] = host_pointer_step(pa)
+            log(f"{HEAD_NAME} M=1 host pointers: {extra['q4_k_m1_host_pointers']}")
             extra["prefill_m512"] = prefill(pa, hm, 20)
             log(f"prefill: {extra['prefill_m512']}")
             extra["decode_8b_ctx2048"] = decode_8b(pa, hm, 20, 5)
@@ -754,10 +758,11 @@ def main() -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(head["ms_per_step"], 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "Q4_0 GEMV M=1, Llama-3-8B projections q,k,v,o,gate,up,down "
+        "config": {"workload": f"{HEAD_NAME} GEMV M=1, Llama-3-8B projections q,k,v,o,gate,up,down "
                                "as one layer's decode step (q/k/v fused, o, gate/up fused, "
                                f"down: 4 launches), {args.layers} rotating layer copies",
-                   "weights": "Q4_0 (18 B / 32), f32 N(0,0.02^2) seeded, libpai_hip encoder",
+                   "weights": f"{HEAD_NAME} (144 B / 256), f32 N(0,0.02^2) seeded, libpai_hip "
+                              f"K-quant encoder",
                    "activations": "f32 N(0,1) resident in HBM",
                    "weight_set_MB": head["weight_set_MB"],
                    "frac_hbm_wall": round(head["GBps"] / HBM_PEAK_GBS, 4),
