@@ -356,6 +356,43 @@ struct Q4_K {
     scales(w, c, d1, m1);
     return fmaf(d1 * x.xs, combine<6>(A), fmaf(8.0f, d1, -m1) * (x.sx0 + x.sx1));
   }
+  /* The scale/min unpack of sub-block j for a lane whose j is fixed (the
+   * GEMV: chunk cb + lane with cb a multiple of 8, so j = lane % 8): one
+   * byte permute gathers byte i = j % 4 of the min/scale word and of the
+   * high-bits word into bytes 0 and 1, and a bit-field insert with a
+   * per-lane mask takes the 6-bit field (j < 4) or its low 4 bits plus
+   * the 2 high bits (j >= 4). Equal to scale_min_k4 for every j. */
+  struct Lane {
+    uint32_t sel, mask, msh;
+  };
+  __device__ static Lane lane_ctx(uint32_t j) {
+    const uint32_t i = j & 3u;
+    const bool lo = j < 4u;
+    Lane l;
+    /* perm(hi = scale or min word, lo = high-bits word): byte 0 <- the
+     * field's low byte (j < 4: byte i of the scale/min word; else byte i
+     * of the high-bits word), byte 1 <- byte i of the scale/min word */
+    l.sel = (lo ? (4u + i) : i) | ((4u + i) << 8) | 0x0C0C0000u;
+    l.mask = lo ? 0x3Fu : 0x0Fu;
+    l.msh = lo ? 0u : 4u;
+    return l;
+  }
+  __device__ static void scales_lane(const Raw &w, const Lane &l, float &d1, float &m1) {
+    const uint32_t ps = __builtin_amdgcn_perm(w.m.y, w.m.w, l.sel);
+    const uint32_t pm = __builtin_amdgcn_perm(w.m.z, w.m.w, l.sel);
+    const uint32_t s = ((ps & l.mask) | ((ps >> 10) & ~l.mask)) & 63u;
+    const uint32_t mn = (((pm >> l.msh) & l.mask) | ((pm >> 10) & ~l.mask)) & 63u;
+    d1 = h2f_lo(w.m.x) * (float)s;
+    m1 = h2f_hi(w.m.x) * (float)mn;
+  }
+  __device__ static float dot_lane(const Raw &w, const Lane &l, const XChunk &x) {
+    const uint32_t s[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+    int32_t A[6];
+    dots0<0, 4>(s, x, A);
+    float d1, m1;
+    scales_lane(w, l, d1, m1);
+    return fmaf(d1 * x.xs, combine<6>(A), fmaf(8.0f, d1, -m1) * (x.sx0 + x.sx1));
+  }
 };
 
 /* ---------------------------------------------------------------- Q6_K */

@@ -195,6 +195,27 @@ __device__ __forceinline__ void x_planes(uint32_t nsc, const float4 (&va)[XI],
   }
 }
 
+/* A format's dot product for a lane whose chunk's position in its
+ * super-block is fixed for the whole launch (chunk cb + lane, cb a
+ * multiple of 8): Q4_K precomputes its scale/min unpack selectors from the
+ * lane once; the other formats take the plain dot. */
+template <class F>
+struct LaneDot {
+  struct Ctx {};
+  __device__ static Ctx make(uint32_t) { return {}; }
+  __device__ static float dot(const typename F::Raw &w, uint32_t c, const Ctx &, const XChunk &x) {
+    return F::dot(w, c, x);
+  }
+};
+template <>
+struct LaneDot<Q4_K> {
+  typedef Q4_K::Lane Ctx;
+  __device__ static Ctx make(uint32_t lane) { return Q4_K::lane_ctx(lane & 7u); }
+  __device__ static float dot(const Q4_K::Raw &w, uint32_t, const Ctx &l, const XChunk &x) {
+    return Q4_K::dot_lane(w, l, x);
+  }
+};
+
 /* Matrices of one launch: up to kMaxMats weights with the same format and
  * column count, multiplied by the same activations (the q/k/v or gate/up
  * projections of a layer). Waves [wave_end[i-1], wave_end[i]) work on
@@ -368,6 +389,8 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[u][t] = 0.0f;
+  /* lanes past the slice end (clamped chunks) are masked below */
+  const typename LaneDot<F>::Ctx lctx = LaneDot<F>::make(lane);
 
   auto compute_block = [&](uint32_t b, const typename F::Raw (&buf)[U]) {
     const uint32_t g = b / steps, s = b % steps;
@@ -393,7 +416,7 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
       xc.sx1 = f.sx1;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float d = F::dot(buf[u], cs + clc, xc);
+        const float d = LaneDot<F>::dot(buf[u], cs + clc, lctx, xc);
         /* a bitwise select, not a branch around the dot product */
         const uint32_t keep = (live && row0 + (uint32_t)(PAIR ? u / 2 : u) < r_end) ? ~0u : 0u;
         acc[u][t] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, d) & keep);
