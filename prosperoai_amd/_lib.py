@@ -65,6 +65,26 @@ SIGNATURES = {
     "pai_hip_dequantize_f32_async": (C.c_int32, [_vp, _vp, C.c_uint64, _vp, _vp, _vp]),
     "pai_gemm_w8_ref_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
     "pai_gemm_w4_ref_f32": (C.c_int32, [C.c_uint64] * 3 + [_vp] * 3 + [C.c_uint64, _vp]),
+    # pai_pai64.h
+    "pai64_crc32": (C.c_uint32, [C.c_uint32, _vp, C.c_uint64]),
+    "pai64_write_file": (C.c_int32, [C.c_char_p, _vp, C.c_uint32, C.POINTER(C.c_uint64)]),
+    "pai64_open": (C.c_int32, [_vp, C.c_uint64, _vp]),
+    "pai64_section": (C.c_void_p, [_vp, C.c_uint32, C.POINTER(C.c_uint64)]),
+    "pai64_verify_section": (C.c_int32, [_vp, C.c_uint32]),
+    "pai64_map_file": (C.c_int32, [C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
+    "pai64_unmap_file": (C.c_int32, [_vp, C.c_uint64]),
+    "pai64_manifest_bytes": (C.c_uint64, [_vp, C.c_uint32]),
+    "pai64_manifest_encode": (C.c_int32, [_vp, C.c_uint32, _vp, C.c_uint64,
+                                          C.POINTER(C.c_uint64)]),
+    "pai64_manifest_decode": (C.c_int32, [_vp, C.c_uint64, _vp, C.c_uint32,
+                                          C.POINTER(C.c_uint32)]),
+    "pai64_qmat_upload": (C.c_int32, [_vp, _vp, C.POINTER(C.c_void_p)]),
+    "pai64_tok_bytes": (C.c_uint64, [_vp, C.c_uint32, C.c_uint32]),
+    "pai64_tok_encode": (C.c_int32, [_vp, _vp, C.c_uint32, _vp, C.c_uint32, _vp, C.c_uint64,
+                                     C.POINTER(C.c_uint64)]),
+    "pai64_tok_index": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint32), _vp, C.c_uint32,
+                                    C.POINTER(C.c_uint64)]),
     "pai_hip_quant_tag": (C.c_int32, [C.c_uint32, _vp]),
     "pai_hip_quant_type": (C.c_uint32, [_vp]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),

@@ -23,7 +23,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c", "pai_qref.c", "pai_v0.c"]
+C_SOURCES = ["pai_hip.c", "pai_gguf.c", "pai_llama.c", "paiq.c", "pai_qref.c", "pai_v0.c", "pai_pai64.c"]
 HIP_SOURCES = ["qlayout.hip", "qgemv.hip", "qgemv_mx.hip", "qgemm.hip", "qdecode.hip",
                "qscratch.hip", "qv0.hip"]
 # qgemm.hip is also compiled once per block format (object name, defines):
