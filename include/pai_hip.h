@@ -314,6 +314,40 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate,
 pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags);
 
 /* ---------------------------------------------------------------------- */
+/* The executor's GEMM branch                                               */
+/* ---------------------------------------------------------------------- */
+
+/* run_gemm's shape rules (scheduler/scheduler.c:280-338) for a GGUF
+ * weight of w_n rows of w_k columns, whose graph value has the logical
+ * shape [w_k][w_n]. Shapes are (rank, dims) of the op's values a, b, c:
+ *   is_gemv: y[m] = A[m,k] x[k] with A the weight: a = [w_n, w_k],
+ *            b = [k], c = [m]; m = w_n, n = 1 output per row;
+ *   a of rank 1 (row vector): y[n] = x[k] W[k,n]: b = [w_k, w_n],
+ *            c = [n] or [1, n]; m = 1;
+ *   otherwise C[m,n] = A[m,k] W[k,n]: a = [m, k], b = [w_k, w_n],
+ *            c = [m, n].
+ * Writes the product's tokens (*m_tokens: rows of activations) and
+ * returns MISMATCH where run_gemm does (rank or extent mismatch), and
+ * also when the weight side differs from the weight's own shape;
+ * INVALID_ARG for NULL shape arrays or out pointers. Host-only; no
+ * counterpart beyond run_gemm's own checks. */
+pai_status_t pai_qgemm_shape_check(int is_gemv, uint32_t a_rank, const uint64_t *a_shape,
+                                   uint32_t b_rank, const uint64_t *b_shape, uint32_t c_rank,
+                                   const uint64_t *c_shape, uint64_t w_n, uint64_t w_k,
+                                   uint64_t *m_tokens);
+
+/* The GEMM/GEMV branch itself for a GGUF-tagged weight: the shape check
+ * above against w's shape, then pai_qgemm_f32 on the activations `act`
+ * (the operand that is not the weight: b for the GEMV form, a
+ * otherwise) into `out` (c), with `flags` as pai_qgemm_f32 (host
+ * pointers, or device pointers with PAI_QGEMM_DEVICE_PTRS). Replaces the
+ * pai_ref_gemm_f32 call of scheduler/scheduler.c:340 for such a weight. */
+pai_status_t pai_qgemm_run(const pai_qmat_t *w, int is_gemv, uint32_t a_rank,
+                           const uint64_t *a_shape, uint32_t b_rank, const uint64_t *b_shape,
+                           uint32_t c_rank, const uint64_t *c_shape, const float *act,
+                           float *out, uint32_t flags);
+
+/* ---------------------------------------------------------------------- */
 /* CPU reference twin                                                       */
 /* ---------------------------------------------------------------------- */
 

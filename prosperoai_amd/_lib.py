@@ -85,6 +85,11 @@ SIGNATURES = {
     "pai64_tok_index": (C.c_int32, [_vp, C.c_uint64, C.POINTER(C.c_uint32),
                                     C.POINTER(C.c_uint32), _vp, C.c_uint32,
                                     C.POINTER(C.c_uint64)]),
+    "pai_qgemm_shape_check": (C.c_int32, [C.c_int, C.c_uint32, _vp, C.c_uint32, _vp,
+                                          C.c_uint32, _vp, C.c_uint64, C.c_uint64,
+                                          C.POINTER(C.c_uint64)]),
+    "pai_qgemm_run": (C.c_int32, [_vp, C.c_int, C.c_uint32, _vp, C.c_uint32, _vp, C.c_uint32,
+                                  _vp, _vp, _vp, C.c_uint32]),
     "pai_hip_quant_tag": (C.c_int32, [C.c_uint32, _vp]),
     "pai_hip_quant_type": (C.c_uint32, [_vp]),
     "pai_hip_op_descriptors": (C.c_void_p, [C.POINTER(C.c_uint32)]),

@@ -733,6 +733,66 @@ pai_status_t pai_qdequant_f32(const pai_qmat_t *w, float *out, uint32_t flags) {
 }
 
 /* ---------------------------------------------------------------------- */
+/* The executor's GEMM branch (scheduler/scheduler.c:280-343)               */
+/* ---------------------------------------------------------------------- */
+
+pai_status_t pai_qgemm_shape_check(int is_gemv, uint32_t a_rank, const uint64_t *a,
+                                   uint32_t b_rank, const uint64_t *b, uint32_t c_rank,
+                                   const uint64_t *c, uint64_t w_n, uint64_t w_k,
+                                   uint64_t *m_tokens) {
+  if (a == NULL || b == NULL || c == NULL || m_tokens == NULL)
+    return fail(PAI_ERR_INVALID_ARG, "NULL shape or output");
+  if (is_gemv) {
+    /* y[m] = A[m,k] * x[k], A the weight ([N][K] rows) */
+    if (a_rank != 2u || b_rank != 1u || c_rank != 1u)
+      return fail(PAI_ERR_MISMATCH, "GEMV ranks %u, %u, %u", a_rank, b_rank, c_rank);
+    if (b[0] != a[1] || c[0] != a[0]) return fail(PAI_ERR_MISMATCH, "GEMV extents");
+    if (a[0] != w_n || a[1] != w_k) return fail(PAI_ERR_MISMATCH, "GEMV matrix is not the weight");
+    *m_tokens = 1u;
+    return PAI_OK;
+  }
+  uint64_t m, k, n;
+  if (a_rank == 1u) {
+    /* row vector: y[n] = x[k] * W[k,n] */
+    m = 1u;
+    k = a[0];
+    if (b_rank != 2u || b[0] != k) return fail(PAI_ERR_MISMATCH, "row-vector operand b");
+    n = b[1];
+    if (c_rank == 1u) {
+      if (c[0] != n) return fail(PAI_ERR_MISMATCH, "row-vector output");
+    } else if (c_rank == 2u) {
+      if (c[0] != 1u || c[1] != n) return fail(PAI_ERR_MISMATCH, "row-vector output");
+    } else {
+      return fail(PAI_ERR_MISMATCH, "row-vector output rank %u", c_rank);
+    }
+  } else {
+    /* C[m,n] = A[m,k] * B[k,n] */
+    if (a_rank != 2u || b_rank != 2u) return fail(PAI_ERR_MISMATCH, "GEMM ranks");
+    m = a[0];
+    k = a[1];
+    n = b[1];
+    if (b[0] != k || c_rank != 2u || c[0] != m || c[1] != n)
+      return fail(PAI_ERR_MISMATCH, "GEMM extents");
+  }
+  if (k != w_k || n != w_n) return fail(PAI_ERR_MISMATCH, "operand b is not the weight");
+  *m_tokens = m;
+  return PAI_OK;
+}
+
+pai_status_t pai_qgemm_run(const pai_qmat_t *w, int is_gemv, uint32_t a_rank,
+                           const uint64_t *a_shape, uint32_t b_rank, const uint64_t *b_shape,
+                           uint32_t c_rank, const uint64_t *c_shape, const float *act,
+                           float *out, uint32_t flags) {
+  if (w == NULL) return fail(PAI_ERR_INVALID_ARG, "NULL weight");
+  uint64_t m = 0;
+  const pai_status_t st = pai_qgemm_shape_check(is_gemv, a_rank, a_shape, b_rank, b_shape,
+                                                c_rank, c_shape, w->n, w->k, &m);
+  if (st != PAI_OK) return st;
+  if (m == 0u) return fail(PAI_ERR_INVALID_ARG, "zero tokens");
+  return pai_qgemm_f32(w, m, act, out, flags);
+}
+
+/* ---------------------------------------------------------------------- */
 /* Registry descriptors                                                     */
 /* ---------------------------------------------------------------------- */
 

@@ -151,6 +151,35 @@ class QMat:
                                         stream or None), "pai_qgemm_f32_async")
 
 
+def _shape(dims) -> tuple:
+    dims = [int(d) for d in dims]
+    return len(dims), (C.c_uint64 * max(len(dims), 1))(*dims)
+
+
+def gemm_shape_check(is_gemv: bool, a_shape, b_shape, c_shape, w_n: int, w_k: int) -> int:
+    """run_gemm's shape rules (scheduler/scheduler.c:280-338) against a
+    weight of w_n rows of w_k columns (pai_qgemm_shape_check); returns the
+    number of activation rows (tokens), raises PaiError(MISMATCH) where
+    run_gemm rejects the shapes."""
+    (ar, a), (br, b), (cr, c) = _shape(a_shape), _shape(b_shape), _shape(c_shape)
+    m = C.c_uint64(0)
+    check(lib().pai_qgemm_shape_check(int(is_gemv), ar, a, br, b, cr, c, w_n, w_k, C.byref(m)),
+          "pai_qgemm_shape_check")
+    return m.value
+
+
+def gemm_run(w: QMat, is_gemv: bool, a_shape, b_shape, c_shape, act: np.ndarray) -> np.ndarray:
+    """The executor's GEMM/GEMV op on a GGUF weight (pai_qgemm_run, host
+    pointers): `act` is the operand that is not the weight; the result has
+    the shape of c."""
+    (ar, a), (br, b), (cr, c) = _shape(a_shape), _shape(b_shape), _shape(c_shape)
+    act = np.ascontiguousarray(act, dtype=np.float32)
+    out = np.empty(tuple(int(d) for d in c_shape), dtype=np.float32)
+    check(lib().pai_qgemm_run(w.handle, int(is_gemv), ar, a, br, b, cr, c, act.ctypes.data,
+                              out.ctypes.data, 0), "pai_qgemm_run")
+    return out
+
+
 def gemm_multi_async(mats: list, x_ptr: int, y_ptrs: list, m: int, flags: int = 0,
                      stream: int = 0) -> None:
     """y_i = x * W_i^T for matrices sharing x, in one fused launch

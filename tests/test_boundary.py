@@ -136,6 +136,61 @@ def test_c_program_against_reference_headers(ref_lib, tmp_path):
     assert "boundary ok: 6 descriptors" in r.stdout
 
 
+def test_gemm_branch_against_reference_executor(ref_lib, tmp_path):
+    """pai_qgemm_shape_check against run_gemm itself (scheduler.c:280-343),
+    driven through one-op graphs in the reference executor: equal statuses
+    on 5488 shape combinations of GEMM and GEMV, and the three accepted
+    forms' results on the dequantized weight equal to the CPU twin."""
+    if not (REF / "scheduler" / "scheduler.h").exists() or shutil.which("gcc") is None:
+        pytest.skip("reference headers or gcc absent")
+    exe = tmp_path / "sched_gemm"
+    libdir = ROOT / "prosperoai_amd" / "lib"
+    refdir = ROOT / "oracle" / "_ref"
+    cmd = ["gcc", "-std=c11", "-Wall", "-Werror", f"-I{REF / 'sdk' / 'include'}", f"-I{REF}",
+           f"-I{REF / 'memory'}", f"-I{ROOT / 'include'}", str(ROOT / "tests" / "c" / "sched_gemm.c"),
+           "-o", str(exe), f"-L{libdir}", "-lpai_hip", str(refdir / "libpairef.so"),
+           f"-Wl,-rpath,{libdir}:{refdir}", "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    assert "statuses: 5488 cases, 54 accepted, 0 differ" in r.stdout
+    assert "run_gemm parity ok" in r.stdout
+
+
+@pytest.mark.parametrize("is_gemv,a,b,c,w,tokens", [
+    (True, [1024, 4096], [4096], [1024], (1024, 4096), 1),
+    (False, [4096], [4096, 1024], [1024], (1024, 4096), 1),
+    (False, [4096], [4096, 1024], [1, 1024], (1024, 4096), 1),
+    (False, [512, 4096], [4096, 14336], [512, 14336], (14336, 4096), 512),
+])
+def test_gemm_branch_accepts_the_llama_forms(is_gemv, a, b, c, w, tokens):
+    assert pa.gemm_shape_check(is_gemv, a, b, c, *w) == tokens
+
+
+@pytest.mark.parametrize("is_gemv,a,b,c,w", [
+    (True, [4096, 1024], [4096], [1024], (1024, 4096)),     # A is [k, n]: not the weight rows
+    (True, [1024, 4096], [4096], [1, 1024], (1024, 4096)),  # GEMV output of rank 2
+    (False, [4096], [4096, 1024], [2, 1024], (1024, 4096)),  # row vector, two output rows
+    (False, [4096], [1024, 4096], [1024], (1024, 4096)),   # B untransposed
+    (False, [8, 4096], [4096, 1024], [1024], (1024, 4096)),  # GEMM output of rank 1
+    (False, [8, 4096], [4096, 1024], [8, 1024], (1000, 4096)),  # another weight
+    (False, [2, 8, 4096], [4096, 1024], [16, 1024], (1024, 4096)),  # rank-3 activations
+])
+def test_gemm_branch_rejects_as_run_gemm(is_gemv, a, b, c, w):
+    with pytest.raises(pa.PaiError, match="MISMATCH"):
+        pa.gemm_shape_check(is_gemv, a, b, c, *w)
+
+
+def test_gemm_branch_argument_errors_without_a_gpu():
+    L = lib()
+    dims = (C.c_uint64 * 2)(4, 4)
+    m = C.c_uint64(0)
+    assert L.pai_qgemm_shape_check(0, 2, None, 2, dims, 2, dims, 4, 4, C.byref(m)) == -1
+    assert L.pai_qgemm_shape_check(0, 2, dims, 2, dims, 2, dims, 4, 4, None) == -1
+    assert L.pai_qgemm_run(None, 0, 2, dims, 2, dims, 2, dims, None, None, 0) == -1
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("m,n,k,gs", [(3, 5, 8, 4), (2, 33, 70, 32), (1, 64, 128, 0), (4, 7, 9, 100)])
 def test_v0_cpu_twins_equal_reference_build(ref_lib, bits, m, n, k, gs):

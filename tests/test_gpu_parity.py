@@ -437,3 +437,38 @@ def test_graph_replays_match_eager():
         a.gemm(x.reshape(1, k))  # eager work between replays
     g.destroy()
     st.destroy()
+
+
+# ------------------------------------------------------------------ the executor's GEMM branch
+@pytest.mark.parametrize("qtype", [12, 14])
+@pytest.mark.parametrize("form,m", [("gemv", 1), ("row", 1), ("row2d", 1), ("gemm", 5),
+                                    ("gemm", 40)])
+def test_gemm_branch_forms(qtype, form, m):
+    """pai_qgemm_run in run_gemm's three forms (scheduler/scheduler.c:280-338)
+    on a 1024 x 4096 weight: bit-equal to pai_qgemm_f32 on the same tokens,
+    and within its tolerance of the oracle's f64 product (16-bit MFMA at 40
+    tokens, the integer-dot kernels below 8). K is kept in one part so that
+    the MFMA results repeat bit for bit (more than two parts add with
+    atomics in arrival order)."""
+    n, k = 1024, 4096
+    say(f"[gpu] gemm branch {form} type={qtype} m={m}")
+    blocks = weights(qtype, n, k, 0xB0 + qtype)
+    w = pa.QMat(qtype, n, k, blocks)
+    x = pa.normal_f32(0xB1 + m, m * k).reshape(m, k)
+    if form == "gemv":
+        shapes = ([n, k], [k], [n])
+    elif form == "row":
+        shapes = ([k], [k, n], [n])
+    elif form == "row2d":
+        shapes = ([k], [k, n], [1, n])
+    else:
+        shapes = ([m, k], [k, n], [m, n])
+    with pa.tuning(gemm_splits=1):
+        y = pa.gemm_run(w, form == "gemv", *shapes, x)
+        direct = w.gemm(x)
+    assert list(y.shape) == shapes[2]
+    assert np.array_equal(y.reshape(m, n).view(np.uint32), direct.view(np.uint32))
+    tol = TOL_F32 if m < pa.MFMA_MIN_M else TOL_F16
+    assert rel_l2(y.reshape(m, n), ob.qgemm_f64(qtype, n, k, blocks, x)) <= tol
+    with pytest.raises(pa.PaiError, match="MISMATCH"):
+        pa.gemm_run(w, form == "gemv", shapes[0], shapes[1], [n + 1], x)
