@@ -168,7 +168,8 @@ def per_launch_times(pa, hm, layers, m: int, plan, reps: int = 50) -> dict:
         def one(sh, r):
             enqueue_entry(pa, layers[r % len(layers)], name, idx, m, x.ptr,
                           [y.ptr for y in ys], sh)
-        one(stream.handle, 0)  # eager first: workspaces are allocated outside capture
+        for r in range(len(layers)):  # eager first: workspaces are allocated outside capture
+            one(stream.handle, r)
         stream.synchronize()
         g = hm.Graph(stream, lambda sh: [one(sh, r) for r in range(reps)])
         g.launch(stream)
