@@ -8,12 +8,13 @@
  * wave owns a contiguous range of rows and walks it block by block, where
  * a block is U rows x one 64-chunk step (lane l takes chunk 64s + l, so
  * one row's loads of a block are one contiguous 1 KiB read). Each lane
- * keeps 8 row-chunk loads in flight (a ring of 8/U blocks, refilled as
- * each block is multiplied), so a 33 MB matrix on 4096 waves is requested
- * in one pass and the dot products overlap the HBM stream.
+ * keeps 4 row-chunk loads in flight (a ring of 4/U blocks, refilled as
+ * each block is multiplied): about 8-16 MB requested across the chip at
+ * any time, enough to keep HBM busy while the dot products overlap the
+ * stream (see kInFlight).
  *
  * Per workgroup:
- *   1. each wave issues the loads of its first 8/U blocks, then all threads
+ *   1. each wave issues the loads of its first 4/U blocks, then all threads
  *      turn the activations of the launch's column slice into digit planes
  *      in LDS (XChunk in qdev.h: six signed 4-bit digit planes of a 24-bit
  *      fixed-point image of x with a per-chunk scale 2^(E-22)). Four
@@ -44,7 +45,17 @@ namespace paik {
 
 constexpr int kWaves = 16;   /* waves per workgroup (one workgroup per CU) */
 constexpr int kWavesSmall = 8; /* for one-token launches with under 2 rows per wave at kWaves */
-constexpr int kInFlight = 8; /* row-chunk loads per lane kept in flight */
+/* Row-chunk loads per lane kept in flight. Deeper rings request more of
+ * the matrix at once than HBM can return in a round trip; the queue that
+ * builds up delays every request behind it, the activation loads that the
+ * dot products wait for included. Measured on the Q4_K decode step
+ * (q/k/v, o, gate/up, down): 8 loads (2 blocks at U = 4, 4 at U = 2)
+ * 7.5 / 5.8 / 15.8 / 10.2 us, 3050 GB/s; 4 loads 6.3 / 5.0 / 14.3 / 9.7 us,
+ * 3340 GB/s; the 8B decode step 1.965 -> 1.836 ms per token. A ring
+ * longer than a wave's blocks also re-reads its last block: q/k/v at 2
+ * blocks per wave took 7.5 us with 4 ring slots against 6.3 with 2. One
+ * slot at U = 2 starves the longer rows (down: 11.9 us). */
+constexpr int kInFlight = 4;
 constexpr size_t kLdsBudget = 65536; /* bytes of LDS per workgroup */
 
 template <int CTRL>
