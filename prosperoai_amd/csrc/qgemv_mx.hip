@@ -73,10 +73,14 @@ constexpr int waves() { return MT <= 2 ? 16 : 8; }
 /* plane-builder passes: 1024 chunk-tokens, four threads each */
 template <int NW>
 constexpr int xit() { return (int)(4u * kMaxChunkTok / (64u * (uint32_t)NW)); }
-/* steps of loads in flight per wave: 8 for Q4_0 (20 bytes a step) at up to
- * 2 tokens, else 6 */
+/* Steps of loads in flight per wave: 2 up to 2 tokens (16-wave
+ * workgroups), else 4. Deeper rings queue more of the matrix than HBM
+ * returns in a round trip and delay every request behind them. Measured
+ * on the Q4_K decode step (q/k/v + o + gate/up + down, us): 2 tokens 58.8
+ * with the earlier 6-step ring, 48.9 with 2, 51.5 with 3; 4 tokens 79.1,
+ * 73.1, 72.9, and 71.9 with 4; 8 tokens 80.5, 81.8, 78.5, 78.2. */
 template <class F, int MT>
-constexpr int ring() { return MT <= 2 && sizeof(typename F::Raw) <= 20 ? 8 : 6; }
+constexpr int ring() { return MT <= 2 ? 2 : 4; }
 
 /* LDS layout: planes [MT][nch][3][32] | zero [32] | scales [MT][nch]
  * float4 {xs * f, sx0, sx1, sx0 + sx1} | partials [2][waves][MT][rows per item]. */
