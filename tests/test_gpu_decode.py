@@ -238,6 +238,9 @@ ATTN_CASES = [
     (16, 2, 256, 128, [1, 77, 128], 1.0),
     (8, 1, 128, 300, [300], 4.0),
     (12, 4, 64, 96, [96], 1.0),            # three q heads per KV head
+    # contexts past 2048 positions (up to 66 chunks to merge), lengths on and
+    # one past chunk boundaries
+    (32, 8, 128, 4200, [129, 640, 2049, 4096, 4097, 4200], 1.0),
 ]
 
 
