@@ -161,6 +161,46 @@ def test_small_batch_parity(qtype, m):
         assert rel_l2(y[i], ref[i]) <= TOL_F32, i
 
 
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("n,k", [(1000, 4096), (777, 7168)])
+def test_gemv_launch_shapes_same_bits(qtype, n, k):
+    """The one-token GEMV's launch shape (rows per group 1, 2 or 4, which
+    sets the ring to 4, 2 or 1 blocks; 8- or 16-wave workgroups; grid
+    size) changes which wave owns a row, never a row's summation order:
+    every shape gives the same bits, within 1e-5 of the reference."""
+    say(f"[gpu] gemv launch shapes type={qtype} n={n} k={k}")
+    blocks = weights(qtype, n, k, 5 * n + qtype)
+    x = pa.normal_f32(41 + k, k).reshape(1, k)
+    w = pa.QMat(qtype, n, k, blocks)
+    y0 = w.gemm(x)
+    assert rel_l2(y0, ob.qgemm_seq(qtype, n, k, blocks, x)) <= TOL_F32
+    shapes = [{"gemv_rows": 1}, {"gemv_rows": 2}, {"gemv_rows": 4}, {"gemv_nw": 8},
+              {"gemv_nw": 16}, {"gemv_wgs": 37}, {"gemv_wgs": 256, "gemv_rows": 1}]
+    for kw in shapes:
+        with pa.tuning(**kw):
+            y = w.gemm(x)
+        assert np.array_equal(y.view(np.uint32), y0.view(np.uint32)), kw
+    w.free()
+
+
+@pytest.mark.parametrize("qtype", [2, 8, 12, 14])
+@pytest.mark.parametrize("m", [2, 3, 4, 7])
+def test_integer_dot_token_groups(qtype, m):
+    """Calls of 2..8 tokens on the integer-dot kernel's token groups (2 or 4
+    tokens per launch) instead of the matrix cores: the reference's bar."""
+    n, k = 257, 4096
+    say(f"[gpu] gemv token groups type={qtype} m={m}")
+    blocks = weights(qtype, n, k, 11 * m + qtype)
+    x = pa.normal_f32(7 * m + k, m * k).reshape(m, k)
+    w = pa.QMat(qtype, n, k, blocks)
+    with pa.tuning(gemv_no_mx=1):
+        y = w.gemm(x)
+    ref = ob.qgemm_seq(qtype, n, k, blocks, x)
+    for i in range(m):
+        assert rel_l2(y[i], ref[i]) <= TOL_F32, i
+    w.free()
+
+
 @pytest.mark.parametrize("qtype", [2, 12])
 def test_batched_decode_llama8b_m8(qtype):
     """Eight tokens at the 8B shapes: q (K = 4096) takes the matrix-core
