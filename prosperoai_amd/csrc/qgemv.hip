@@ -54,7 +54,8 @@ constexpr int kWavesSmall = 8; /* for one-token launches with under 2 rows per w
  * 3340 GB/s; the 8B decode step 1.965 -> 1.836 ms per token. A ring
  * longer than a wave's blocks also re-reads its last block: q/k/v at 2
  * blocks per wave took 7.5 us with 4 ring slots against 6.3 with 2. One
- * slot at U = 2 starves the longer rows (down: 11.9 us). */
+ * slot at U = 2 starves the longer rows (down: 11.9 us). 16-wave
+ * workgroups take half of this (see PD). */
 constexpr int kInFlight = 4;
 constexpr size_t kLdsBudget = 65536; /* bytes of LDS per workgroup */
 
@@ -379,7 +380,10 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
   x_load<MT, XI>(x, v.k, ntok, cs, nsc, xa, xb);
   float4 ga[XI], gb[XI]; /* NORM: gamma in the same layout (one slice covers the row) */
   if constexpr (NORM) x_load<1, XI>(a.y[kNormGammaSlot], v.k, 1u, cs, nsc, ga, gb);
-  constexpr int PD = kInFlight / U;
+  /* 16-wave workgroups run twice the waves of the 8-wave ones, so each of
+   * their lanes keeps half the loads in flight (q/k/v: 6.2 -> 5.9 us) */
+  constexpr int kIF = NW == 16 ? kInFlight / 2 : kInFlight;
+  constexpr int PD = kIF / U > 0 ? kIF / U : 1;
   typename F::Raw buf[PD][U];
   /* Every load below is unconditional (blocks past the wave's last one
    * re-read that block, an L2 hit), so each wave issues the same sequence
