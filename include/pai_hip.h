@@ -219,9 +219,8 @@ pai_status_t pai_qmat_upload_gguf(pai_qmat_t **out, const pai_gguf_dir_t *d,
  *    need |x| < 65504 (larger values become inf); bf16 has the f32 range.
  *    Each matrix keeps a device workspace for a 16-bit copy of up to 1024
  *    tokens of x, allocated by the first such call made outside stream
- *    capture; single-matrix calls of up to 32 tokens round x inside the
- *    GEMM instead and use no copy (same rounding, same bits). Workspaces
- *    only grow: a buffer replaced by a larger one stays
+ *    capture; calls of up to 32 tokens round x inside the GEMM instead
+ *    and use no copy (same rounding, same bits). Workspaces only grow: a buffer replaced by a larger one stays
  *    allocated until pai_qmat_free, because a HIP graph captured earlier
  *    still refers to it. Destroy every graph that used a handle before
  *    freeing the handle.

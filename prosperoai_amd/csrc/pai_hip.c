@@ -509,13 +509,23 @@ static void *part_workspace(const pai_qmat_t *cw, const paik_qview_t *const *vs,
   return p;
 }
 
-/* Matrices sharing x in one MFMA launch (the 16-bit path; the
- * register-staged fallback launches them one by one). */
+/* MFMA calls of up to this many tokens round x to 16 bits inside the GEMM
+ * (register-staged activations: same tiles, split plan, rounding and
+ * MFMA order, so the same bits) instead of in a conversion launch before
+ * it. Measured on the Q4_K batched decode step at 32 tokens: o 15.5 ->
+ * 14.1 us, down 24.0 -> 23.0, the q/k/v launch 18.5 -> 16.9; at 16 tokens
+ * q/k/v 17.3 -> 15.6. Larger calls take the 16-bit copy, which the
+ * activation tiles of many token tiles share. */
+#define PAI_DIRECT_TOKENS 32u
+
+/* Matrices sharing x in one MFMA launch. */
 static pai_status_t launch_mfma_multi(const pai_qmat_t *const *ws, uint32_t count, uint64_t m,
                                       const float *x, float *const *ys, const float *gate,
                                       uint32_t flags, hipStream_t s) {
   uint64_t wb = 0, pb = 0;
-  void *x16 = paik_tune.gemm_no_x16 != 0 ? NULL : x16_workspace(ws[0], m, s, &wb);
+  void *x16 = paik_tune.gemm_no_x16 != 0 || m <= PAI_DIRECT_TOKENS
+                  ? NULL
+                  : x16_workspace(ws[0], m, s, &wb);
   const paik_qview_t *vs[4];
   for (uint32_t i = 0; i < count; ++i) vs[i] = &ws[i]->view;
   void *part = gate != NULL ? NULL : part_workspace(ws[0], vs, count, m, s, &pb);
@@ -529,26 +539,11 @@ static pai_status_t launch_mfma(const pai_qmat_t *w, uint64_t m, const float *x,
   return launch_mfma_multi(&w, 1u, m, x, &y, gate, flags, s);
 }
 
-/* Single-matrix MFMA calls of up to this many tokens round x to 16 bits
- * inside the GEMM (register-staged activations, same tile and split plan,
- * same rounding) instead of in a conversion launch before it: measured on
- * the Q4_K batched decode step, o at 32 tokens 15.5 -> 14.1 us, down
- * 24.0 -> 23.0, down at 8 tokens 19.5 -> 18.3. Multi-matrix calls keep the
- * 16-bit copy, which their one launch shares (the register-staged path
- * runs the matrices one by one: q/k/v at 32 tokens 18.5 -> 44.3 us). */
-#define PAI_DIRECT_TOKENS 32u
 
 static pai_status_t launch(const pai_qmat_t *w, uint64_t m, const float *x, float *y,
                            uint32_t flags, hipStream_t s) {
   if (gemv_call(w, m, flags)) {
     const int e = paik_gemv(&w->view, (uint32_t)m, x, y, s);
-    return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
-  }
-  if (m <= PAI_DIRECT_TOKENS) {
-    const paik_qview_t *v = &w->view;
-    const int e = paik_gemm_mfma_multi(&v, &y, 1u, (uint32_t)m, x, NULL,
-                                       (flags & PAI_QGEMM_MFMA_BF16) != 0u, NULL, 0u, NULL, 0u, 0,
-                                       s);
     return e == 0 ? PAI_OK : map_hip((hipError_t)e, "kernel launch");
   }
   return launch_mfma(w, m, x, y, NULL, flags, s);
@@ -660,11 +655,13 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
   if (m <= PAI_X16_TOKENS && paik_tune.gemm_no_x16 == 0 &&
       paik_gemm_x16_splits(&w_up->view, (uint32_t)m) > 1u) {
     uint64_t wb = 0, pb = 0;
-    void *x16 = x16_workspace(w_gate, m, s, &wb);
+    const int direct = m <= PAI_DIRECT_TOKENS; /* x rounded inside the GEMM */
+    void *x16 = direct ? NULL : x16_workspace(w_gate, m, s, &wb);
     const paik_qview_t *vs[2] = {&w_gate->view, &w_up->view};
     const uint64_t need = paik_gemm_part_bytes(vs, 2u, (uint32_t)m);
     void *part = part_workspace(w_gate, vs, 2u, m, s, &pb);
-    if (x16 != NULL && wb >= m * w_gate->k * 2u && part != NULL && need > 0u && pb >= need) {
+    if ((direct || (x16 != NULL && wb >= m * w_gate->k * 2u)) && part != NULL && need > 0u &&
+        pb >= need) {
       float *outs[2] = {h, h};
       const int e = paik_gemm_mfma_multi(vs, outs, 2u, (uint32_t)m, x, NULL,
                                          (flags & PAI_QGEMM_MFMA_BF16) != 0u, x16, wb, part, pb,
@@ -676,7 +673,7 @@ pai_status_t pai_qgemm_f32_gate_up_async(const pai_qmat_t *w_gate, const pai_qma
   if (st != PAI_OK) return st;
   /* the up launch reads the 16-bit copy of x the gate launch just made,
    * when that holds every token (one conversion instead of two) */
-  if (m <= PAI_X16_TOKENS && paik_tune.gemm_no_x16 == 0) {
+  if (m > PAI_DIRECT_TOKENS && m <= PAI_X16_TOKENS && paik_tune.gemm_no_x16 == 0) {
     uint64_t wb = 0;
     void *x16 = x16_workspace(w_gate, m, s, &wb);
     if (x16 != NULL && wb >= ((m + 255u) & ~(uint64_t)255u) * w_gate->k * 2u) {

@@ -296,14 +296,27 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
   constexpr int kXsHalves = 4 * TT * kXPitch >= kTBytes ? TT * kXPitch : kTBytes / 4;
   __shared__ __attribute__((aligned(16))) uint16_t Xs[2][kXsHalves];
 
-  const paik_qview_t &v = a.v;
   /* tile of this workgroup: XCD-major numbering (see the top of the file) */
   const uint32_t logical = (blockIdx.x % kXcds) * a.per_xcd + blockIdx.x / kXcds;
   const uint32_t ntile = a.tiles_n * a.tiles_m;
   if (logical >= ntile * a.splits) return;
   const uint32_t split = logical / ntile, tile = logical % ntile;
   const uint32_t tn = tile % a.tiles_n, tm = tile / a.tiles_n;
-  const uint32_t n0 = tn * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
+  /* the matrix owning row tile tn (multi-matrix launches, as k_gemm_x16) */
+  paik_qview_t v = a.v;
+  float *ybase = a.y;
+  uint32_t tl = tn, rows_before = 0, cum = 0;
+#pragma unroll
+  for (int i = 1; i < kGemmMats; ++i) {
+    cum += a.mv[i - 1].n;
+    if ((uint32_t)i < a.count && tn >= a.tile_end[i - 1]) {
+      v = a.mv[i];
+      ybase = a.my[i];
+      tl = tn - a.tile_end[i - 1];
+      rows_before = cum;
+    }
+  }
+  const uint32_t n0 = tl * (uint32_t)RWG, m0 = tm * (uint32_t)TT;
   const uint32_t nchunks = v.k >> 5;
   const uint32_t s0 = split * a.steps_per_split; /* < number of steps */
   const uint32_t s1 = s0 + a.steps_per_split;     /* multiple of 4, may pass the row end */
@@ -466,7 +479,9 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
    * one token. */
   const bool split_k = a.splits > 1u;
   const bool gated = a.gate != nullptr && !split_k;
-  float *const pbase = a.part != nullptr ? a.part + (size_t)split * a.m * v.n : nullptr;
+  float *const pbase = a.part != nullptr ? a.part + (size_t)a.splits * a.m * rows_before +
+                                                (size_t)split * a.m * v.n
+                                          : nullptr;
   float *Ts = reinterpret_cast<float *>(&Xs[0][0]) + wave * (32 * kTP);
   constexpr int TPI = 64 / RW; /* tokens per read-out instruction */
   const uint32_t orow = n0 + (uint32_t)(RW * wave + (lane % RW));
@@ -502,9 +517,9 @@ __global__ void __launch_bounds__(64 * NW, 1) k_gemm(GemmArgs a) {
       if (tok < a.m && orow < v.n) {
         const size_t at = (size_t)tok * v.n + orow;
         if (pbase != nullptr) pbase[at] = val;
-        else if (split_k) unsafeAtomicAdd(a.y + at, val);
-        else if (gated) a.y[at] = silu_mul(gv[q], val);
-        else a.y[at] = val;
+        else if (split_k) unsafeAtomicAdd(ybase + at, val);
+        else if (gated) ybase[at] = silu_mul(gv[q], val);
+        else ybase[at] = val;
       }
     }
   }
@@ -889,6 +904,53 @@ static hipError_t launch_reduce(float *part, float *const *ys, const uint32_t *n
   const size_t blocks = (cum + 255u) / 256u;
   k_split_reduce<><<<dim3((unsigned)(blocks < 4096u ? blocks : 4096u)), 256, 0, s>>>(r);
   return hipGetLastError();
+}
+
+/* Several matrices sharing x in one register-staged launch (as launch_x16
+ * without the 16-bit copy): split parts go to the workspace and one reduce
+ * launch sums them in order (silu_pair: forms silu(gate) * up). */
+template <class F, int TT, int NW, int RWG, int XB>
+static hipError_t launch_tt_multi(const paik_qview_t *const *vs, float *const *ys, uint32_t count,
+                                  uint32_t m, const float *x, bool bf16, float *part,
+                                  size_t part_bytes, bool silu_pair, hipStream_t s) {
+  GemmArgs a;
+  memset(&a, 0, sizeof a);
+  a.v = *vs[0];
+  a.x = x;
+  a.y = ys[0];
+  a.m = m;
+  a.count = count;
+  uint32_t tiles = 0;
+  size_t rows = 0;
+  uint32_t ns[kGemmMats];
+  for (uint32_t i = 0; i < count; ++i) {
+    a.mv[i] = *vs[i];
+    a.my[i] = ys[i];
+    tiles += (vs[i]->n + (uint32_t)RWG - 1u) / (uint32_t)RWG;
+    a.tile_end[i] = tiles;
+    ns[i] = vs[i]->n;
+    rows += vs[i]->n;
+  }
+  a.tiles_n = tiles;
+  plan_grid(a, RWG, TT);
+  a.x_bytes = (uint32_t)((size_t)m * a.v.k * 4u);
+  const bool parts = a.splits > 1u && part != nullptr &&
+                     (size_t)a.splits * m * rows * 4u <= part_bytes;
+  if (silu_pair && !parts) return hipErrorInvalidValue;
+  if (parts) {
+    a.part = part;
+  } else if (a.splits > 1u) {
+    for (uint32_t i = 0; i < count; ++i) {
+      const hipError_t e = zero_fill(ys[i], (size_t)m * vs[i]->n, s);
+      if (e != hipSuccess) return e;
+    }
+  }
+  const dim3 grid(a.per_xcd * kXcds), block(64 * NW);
+  if (bf16) k_gemm<F, true, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
+  else k_gemm<F, false, TT, NW, RWG, XB><<<grid, block, 0, s>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !parts) return e;
+  return launch_reduce(part, ys, ns, count, m, a.splits, s, silu_pair);
 }
 
 template <class F, int TT, int NW, int RWG, int XB>
@@ -1489,6 +1551,10 @@ static hipError_t launch_gemm(const paik_qview_t *const *vs, float *const *ys, u
                                                    part_bytes, silu_pair, s)
                       : launch_x16<F, 0, 8, 0>(vs, yt, count, mt, xt, x16, gt, bf16, part,
                                                part_bytes, silu_pair, s);
+    } else if ((count > 1u || silu_pair) && mt <= 32u && gt == nullptr) {
+      /* up to 32 tokens: the matrices share one register-staged launch */
+      e = launch_tt_multi<F, 32, 8, 256, 2>(vs, yt, count, mt, xt, bf16, part, part_bytes,
+                                            silu_pair, s);
     } else {
       if (silu_pair) return hipErrorInvalidValue; /* the pair form needs the 16-bit path */
       for (uint32_t i = 0; i < count && e == hipSuccess; ++i)
