@@ -87,3 +87,31 @@ def test_noalloc_rejects_k_above_scratch():
     for b in (x, y):
         b.free()
     w.free()
+
+
+@pytest.mark.parametrize("qtype", [pa.Q4_K, pa.Q6_K, pa.Q8_0, pa.Q4_0])
+def test_noalloc_copy_matches_register_tiles(qtype):
+    """Up to 32 tokens the allocating entry rounds x to 16 bits inside the
+    register-staged GEMM (activations requested two steps ahead), while this
+    entry first copies x to 16 bits in its scratch and stages it by DMA. Both
+    round x and the weights the same way and accumulate in the same order,
+    so with K in one part the outputs are identical."""
+    pa.init()
+    n, k = 1000, 4096
+    say(f"[gpu] noalloc copy vs register tiles type={qtype}")
+    blocks = pa.quantize(qtype, pa.normal_f32(0x7B00 + qtype, n * k, 0.0, 0.02).reshape(n, k))
+    w = pa.QMat(qtype, n, k, blocks)
+    xh = pa.normal_f32(0x7B10 + qtype, 32 * k)
+    x = hm.DeviceBuffer.from_array(xh)
+    y_ref, y_na = hm.DeviceBuffer(4 * 32 * n), hm.DeviceBuffer(4 * 32 * n)
+    with pa.tuning(gemm_splits=1):
+        for m in (32, 9, 17):
+            want = run("pai_qgemm_f32_async", w, x, y_ref, m, n)
+            got = run("pai_qgemm_f32_noalloc_async", w, x, y_na, m, n)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), m
+    rows = np.arange(3, n, 31)
+    ref = ob.qgemm_f64(qtype, len(rows), k, blocks[rows], xh[:17 * k].reshape(17, k))
+    assert rel_l2(got[:, rows], ref) <= TOL_F16
+    for b in (x, y_ref, y_na):
+        b.free()
+    w.free()
