@@ -258,10 +258,31 @@ constexpr int kNormGammaSlot = kMaxMats - 1;
  * two parts so that nothing waits for the reduction before the planes are
  * built: rms_begin turns x into x * gamma and leaves each wave's partial
  * sum of squares (lanes in a fixed order) in red[]; after the barrier that
- * publishes the planes, rms_end adds the waves in order and forms rms,
- * which scales every finished dot product. Against the reference's
+ * publishes the planes, rms_end adds the waves in a fixed tree and forms
+ * rms, which scales every finished dot product. Against the reference's
  * per-element (x * gamma) * rms this moves one rounding, O(2^-24)
- * relative. */
+ * relative. The double arithmetic sits on every wave's path to its first
+ * dot product (q/k/v with the norm: 7.0-7.1 us, 6.0-6.3 in a timing build
+ * with rms taken as 1), so it is kept short: a wave adds its lanes within
+ * 16-lane rows by DPP and reads the four row sums with readlane (in place
+ * of six LDS shuffles), rms_end adds the waves as a tree, and 1/K is formed
+ * before the barrier (gate/up with the norm 15.5 -> 15.0 us; the 8B decode
+ * step 1.827 -> 1.816 ms per token). Formed after the first row group
+ * instead, rms only moved the same chain to the end (q/k/v 7.1 -> 7.5 us). */
+template <int CTRL>
+__device__ __forceinline__ double dppd(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 template <int XI>
 __device__ __forceinline__ void rms_begin(float4 (&va)[XI], float4 (&vb)[XI],
                                           const float4 (&ga)[XI], const float4 (&gb)[XI],
@@ -278,8 +299,15 @@ __device__ __forceinline__ void rms_begin(float4 (&va)[XI], float4 (&vb)[XI],
     acc += (double)vb[it].z * (double)vb[it].z;
     acc += (double)vb[it].w * (double)vb[it].w;
   }
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = acc;
+  /* every lane of a 16-lane row ends with the row's sum (each step adds
+   * the same two partial sums in every lane) */
+  acc += dppd<kQuadXor1>(acc);
+  acc += dppd<kQuadXor2>(acc);
+  acc += dppd<0x141>(acc); /* row_half_mirror */
+  acc += dppd<0x140>(acc); /* row_mirror */
+  const double wsum = (readlane_d(acc, 0) + readlane_d(acc, 16)) +
+                      (readlane_d(acc, 32) + readlane_d(acc, 48));
+  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = wsum;
   auto mul = [](float4 x, float4 g) {
     return make_float4(x.x * g.x, x.y * g.y, x.z * g.z, x.w * g.w);
   };
@@ -290,11 +318,16 @@ __device__ __forceinline__ void rms_begin(float4 (&va)[XI], float4 (&vb)[XI],
   }
 }
 template <int NW>
-__device__ __forceinline__ float rms_end(const double *red, uint32_t n, float eps) {
-  double tot = 0.0;
+__device__ __forceinline__ float rms_end(const double *red, double inv_n, float eps) {
+  static_assert((NW & (NW - 1)) == 0, "waves: a power of two");
+  double p[NW];
 #pragma unroll
-  for (int w = 0; w < NW; ++w) tot += red[w];
-  return 1.0f / sqrtf((float)(tot / (double)n) + eps);
+  for (int w = 0; w < NW; ++w) p[w] = red[w];
+#pragma unroll
+  for (int h = NW / 2; h >= 1; h /= 2)
+#pragma unroll
+    for (int w = 0; w < h; ++w) p[w] += p[w + h];
+  return 1.0f / sqrtf((float)(p[0] * inv_n) + eps);
 }
 
 /* Weight loads of a block are issued for all its lanes and rows with
@@ -393,11 +426,13 @@ __global__ void __launch_bounds__(64 * NW) k_gemv(GemvArgs a, const float *__res
 #pragma unroll
   for (int p = 0; p < PD; ++p) load_block((uint32_t)p, buf[p]);
 
-  __shared__ double red[NORM ? NW : 1];
+  __shared__ __attribute__((aligned(16))) double red[NORM ? NW : 1];
+  /* 1/K in double, formed while the activations are in flight */
+  const double inv_k = NORM ? 1.0 / (double)v.k : 1.0;
   if constexpr (NORM) rms_begin<XI>(xa, xb, ga, gb, red);
   x_planes<MT, XI>(nsc, xa, xb, xp, xf);
   __syncthreads();
-  const float rms = NORM ? rms_end<NW>(red, v.k, a.eps) : 1.0f;
+  const float rms = NORM ? rms_end<NW>(red, inv_k, a.eps) : 1.0f;
 
   float acc[U][MT];
 #pragma unroll
